@@ -1,0 +1,291 @@
+"""Benchmark: TinyLlama-1.1B-shape fp16 batch-1 decode at context 512 (C2)
+through the ``hip`` plugin on one MI355X.
+
+A step is one greedy decode token.  The model is random-init (seeded,
+N(0, 0.02), norms = 1), the prompt is 512 uniform random ids.  The program:
+prefill of the prompt (timed separately), then ``--warmup`` untimed decode
+steps, then exactly ``--steps`` timed decode steps bracketed by device
+synchronisation.  Decoding uses the device-resident greedy loop (the KV
+caches are donated and updated in place; token, position and masks advance
+on the device; no host round trip per token).
+
+Besides the JSON line's ``value`` (decode tok/s), ``roofline`` describes the
+dominant kernel -- the fused RMSNorm + gate/up GEMV + SiLU -- from per-launch
+HIP-event timings of the real decode plan, and ``cpu_baseline`` times the
+NumPy oracle (the reference's cpu plugin algorithm) on a bounded sample of
+the same workload on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "chomik-grad_amd"), str(ROOT)]
+
+METRIC = "decode tok/s + % HBM roofline, TinyLlama-1.1B-shape fp16 bs=1 ctx512"
+HBM_PEAK_GBPS = 8000.0
+PROMPT = 512
+
+
+def log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def kernel_label(step) -> str:
+    from chomikgrad._planner import K_GEMV, KIND_NAMES
+
+    if step.kind != K_GEMV:
+        return KIND_NAMES[step.kind]
+    tags = []
+    if step.attrs["prologue"]:
+        tags.append("rms_norm")
+    if step.attrs["silu"]:
+        tags.append("silu_mul")
+    if any(s["res"] is not None for s in step.attrs["segments"]):
+        tags.append("residual")
+    return "gemv[" + "+".join(tags) + "]" if tags else "gemv"
+
+
+def algorithmic_bytes(step) -> int:
+    """Bytes a kernel must move at minimum: every operand read once, every
+    result written once (KV writes in place touch one row per head)."""
+    from chomikgrad._planner import K_GEMV, K_KV_WRITE
+
+    if step.kind == K_GEMV:
+        total = sum(pv.size * pv.itemsize for pv in step.reads())
+        return total + sum(pv.size * pv.itemsize for pv in {id(o.storage): o for o in step.outs}.values())
+    if step.kind == K_KV_WRITE and step.attrs.get("in_place"):
+        cache, x, w = step.ins
+        row = cache.shape[0] * cache.shape[1] * cache.shape[3] * cache.itemsize
+        return w.size * w.itemsize + x.size * x.itemsize + row
+    total = sum(pv.size * pv.itemsize for pv in step.reads())
+    return total + sum(pv.size * pv.itemsize for pv in step.outs)
+
+
+def weights_bytes(config, itemsize: int) -> int:
+    from chomikgrad.llama import required_weight_shapes
+
+    shapes = required_weight_shapes(config)
+    total = 0
+    for name, shape in shapes.items():
+        if name == "model.embed_tokens.weight":
+            total += shape[1] * itemsize  # one embedding row per token
+        else:
+            total += int(np.prod(shape)) * itemsize
+    return total
+
+
+def cpu_baseline(config, weights, dtype, context: int, first_position: int, steps: int) -> dict:
+    """Oracle decode steps on the host: the reference's NumPy cpu-plugin
+    algorithm, float16, with zero-filled caches of the real context length.
+    fp16 np.matmul is NumPy's single-threaded loop, so one core is used."""
+    import oracle  # noqa: F401  (the checker, timed as the CPU baseline)
+    from chomikgrad import Tensor, get_compiler
+    from chomikgrad.llama import LlamaDecoderStep, _rope_rotations, decode_masks
+
+    compiler = get_compiler("cpu")
+    kv = (1, config.num_key_value_heads, context, config.head_size)
+    caches = [np.zeros(kv, dtype=dtype) for _ in range(2 * config.num_hidden_layers)]
+    decoder = LlamaDecoderStep(config, weights, cache_length=context, dtype=dtype)
+    seconds = []
+    token = 1
+    for step in range(steps):
+        position = first_position + step
+        attention, write = decode_masks(position, context, dtype)
+        leaves = [Tensor(np.array([[token]], np.int32), copy=False),
+                  Tensor(_rope_rotations(1, config.head_size, config.rope_theta, dtype, offset=position), copy=False),
+                  Tensor(attention, copy=False), Tensor(write, copy=False)]
+        cache_tensors = [Tensor(c, copy=False) for c in caches]
+        outputs = decoder(*leaves, list(zip(cache_tensors[::2], cache_tensors[1::2])))
+        started = time.perf_counter()
+        result = compiler.compile([o._node for o in outputs]).run()
+        token = int(np.asarray(result[0]).argmax())
+        seconds.append(time.perf_counter() - started)
+        caches = [np.asarray(c) for c in result[1:]]
+    per_token = statistics.mean(seconds)
+    return {
+        "value": round(1.0 / per_token, 4),
+        "unit": "tok/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{steps} fp16 decode steps of the C2 model at positions {first_position}.."
+                   f"{first_position + steps - 1}, context {context}, zero-filled caches "
+                   f"({per_token:.2f} s/token; host has {len(os.sched_getaffinity(0))} cores, "
+                   "fp16 NumPy matmul uses one)"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=127)
+    parser.add_argument("--warmup", type=int, default=8)
+    parser.add_argument("--timing-runs", type=int, default=4, help="decode steps timed per kernel")
+    parser.add_argument("--cpu-steps", type=int, default=3, help="oracle decode steps for the CPU baseline")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs every kernel on a single MI355X and has no "
+              f"collective path (--gpus {args.gpus} requested)", file=sys.stderr)
+        return 2
+    if args.steps < 1:
+        raise SystemExit("--steps must be positive")
+
+    from chomikgrad import get_compiler, synthetic
+    from chomikgrad.llama import _rope_rotations, decode_masks
+    from chomikgrad.runtime import LlamaRuntime
+
+    spec = synthetic.TINYLLAMA
+    config, dtype = spec.config, spec.dtype
+    hip = get_compiler("hip")
+    device = hip.device
+    log(f"device {device.info}")
+    started = time.perf_counter()
+    host = synthetic.host_weights(config, dtype, seed=0)
+    weights = synthetic.weights_as_tensors(host)
+    log(f"weights generated in {time.perf_counter() - started:.1f} s")
+    runtime = LlamaRuntime(config, weights, compiler="hip", dtype=dtype)
+    prompt = synthetic.prompt_ids(config.vocab_size, PROMPT, seed=0)
+    context = PROMPT + 1 + args.warmup + args.steps + args.timing_runs
+
+    # Prefill (compile + one warm run, then one timed run).
+    runtime.prefill(prompt, context)
+    device.synchronize()
+    log("prefill compiled")
+    t0 = time.perf_counter()
+    logits, caches = runtime.prefill(prompt, context)
+    device.synchronize()
+    prefill_seconds = time.perf_counter() - t0
+    log(f"prefill {PROMPT} tokens: {prefill_seconds * 1e3:.1f} ms")
+
+    history = device.empty((1 + args.warmup + args.steps + args.timing_runs,), np.int32)
+    token = device.empty((1, 1), np.int32)
+    device.greedy_advance(logits, token, history=history, step=0)
+    attention_host, write_host = decode_masks(PROMPT, context, dtype)
+    position = device.array(np.asarray(PROMPT, dtype=np.int32))
+    attention = device.array(attention_host)
+    write = device.array(write_host)
+    program, nodes = runtime._decoder(context, PROMPT, caches, donate=True)
+    rotation = device.array(_rope_rotations(1, config.head_size, config.rope_theta, dtype, offset=PROMPT))
+    bindings = dict(zip(nodes, [token, rotation, attention, write, position, *caches]))
+    if nodes[1] in program.inputs:
+        raise RuntimeError("the decode program does not lower RoPE; the resident loop needs it")
+    logits_out = device.empty((1, config.vocab_size), dtype)
+    log(f"decode plan: {program.kernel_count} kernels per token")
+
+    step_index = 1
+
+    def decode(count: int) -> None:
+        nonlocal step_index
+        for _ in range(count):
+            program.run(bindings, out=[logits_out])
+            device.greedy_advance(logits_out, token, history=history, step=step_index, position=position,
+                                  attention_mask=attention, write_mask=write, cache_length=context)
+            step_index += 1
+
+    decode(args.warmup)
+    device.synchronize()
+    lib = hip.lib
+    start_event, stop_event = ctypes.c_void_p(), ctypes.c_void_p()
+    lib.call("chip_event_create", ctypes.byref(start_event))
+    lib.call("chip_event_create", ctypes.byref(stop_event))
+    device.synchronize()
+    wall0 = time.perf_counter()
+    lib.call("chip_event_record", start_event)
+    decode(args.steps)
+    lib.call("chip_event_record", stop_event)
+    device.synchronize()
+    wall = time.perf_counter() - wall0
+    gpu_ms = ctypes.c_float(0.0)
+    lib.call("chip_event_elapsed_ms", start_event, stop_event, ctypes.byref(gpu_ms))
+    first_timed_position = PROMPT + args.warmup
+    tokens = device.to_numpy(history).tolist()
+    log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, events {gpu_ms.value:.2f} ms")
+
+    # Per-kernel durations of the same decode plan (direct launches bracketed
+    # by HIP events on the library stream), a few steps further on.
+    steps = program._planned.steps
+    durations = {}
+    byte_counts = {}
+    for _ in range(args.timing_runs):
+        ms = (ctypes.c_float * len(steps))()
+        # same slots as the timed loop (already bound): one more decode step
+        lib.call("chip_plan_time_steps", program._plan, ms, ctypes.c_int64(len(steps)))
+        device.greedy_advance(logits_out, token, history=None, step=0, position=position,
+                              attention_mask=attention, write_mask=write, cache_length=context)
+        for step, value in zip(steps, ms):
+            label = kernel_label(step)
+            durations.setdefault(label, []).append(value)
+            byte_counts.setdefault(label, []).append(algorithmic_bytes(step))
+    device.synchronize()
+    breakdown = {
+        label: {"launches_per_token": len(values) // args.timing_runs,
+                "avg_us": round(1e3 * statistics.mean(values), 3),
+                "us_per_token": round(1e3 * sum(values) / args.timing_runs, 2),
+                "gbps": round(statistics.mean(byte_counts[label]) / (statistics.mean(values) * 1e-3) / 1e9, 1)}
+        for label, values in durations.items()
+    }
+    dominant = max(breakdown, key=lambda k: breakdown[k]["us_per_token"])
+    dom_bytes = statistics.mean(byte_counts[dominant])
+    dom_us = breakdown[dominant]["avg_us"]
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+
+    decode_tps = args.steps / wall
+    positions = np.arange(first_timed_position, first_timed_position + args.steps)
+    kv_bytes = 2 * config.num_hidden_layers * config.num_key_value_heads * config.head_size * 2
+    bytes_per_token = float(np.mean(weights_bytes(config, 2) + kv_bytes * (positions + 1) + kv_bytes))
+    step_gbps = bytes_per_token * decode_tps / 1e9
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        log("timing the NumPy oracle on the host (bounded sample)")
+        baseline = cpu_baseline(config, weights, dtype, context, first_timed_position, args.cpu_steps)
+
+    result = {
+        "metric": METRIC,
+        "value": round(decode_tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random-init weights N(0,0.02), norms=1; uniform random prompt ids)",
+        "config": {
+            "workload": "C2: TinyLlama-1.1B-shape fp16 greedy decode, batch 1, 512-token prompt",
+            "prompt": PROMPT, "context": context, "timed_positions": [int(positions[0]), int(positions[-1])],
+            "decode_loop": "device-resident greedy (donated KV caches, no host round trip per token)",
+            "kernels_per_token": program.kernel_count + 1,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": dominant, "bytes_per_launch": int(dom_bytes), "avg_launch_us": dom_us,
+        },
+        "cpu_baseline": baseline,
+        "step_roofline": {"bytes_per_token": int(bytes_per_token), "achieved_gbps": round(step_gbps, 1),
+                          "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
+        "gpu_event_ms_per_step": round(gpu_ms.value / args.steps, 4),
+        "prefill_tok_per_s": round(PROMPT / prefill_seconds, 1),
+        "kernel_breakdown": breakdown,
+        "first_tokens": tokens[:16],
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,269 @@
+"""Generation driver: the counterpart of the reference's ``TinyLlamaRuntime``
+(examples/generate_tinyllama.py:165-263) for in-memory weights.
+
+``LlamaRuntime.generate`` follows ``_generate_loaded``
+(generate_tinyllama.py:678-887): context = prompt + max_new_tokens; the first
+token comes from the prefill program; then ``max_new_tokens - 1`` decode
+steps at ``position = len(tokens) - 1``; prefill programs are cached by
+``(prompt_len, context)`` and decode programs by ``context``.  Two loops:
+
+* ``loop="reference"`` -- the reference's per-step protocol on any compiler:
+  host-built token, rotation, masks and position are uploaded with
+  ``device.array`` every step, caches are functional, and every token is
+  copied to the host by ``device.argmax`` (sample_native_token,
+  generate_tinyllama.py:146-162).
+* ``loop="resident"`` (``hip`` only, greedy) -- only the token, position and
+  KV caches feed each step, and all of them stay on the device: the caches
+  are donated and updated in place, and one queued ``greedy_advance`` writes
+  the next token, position and masks.  The host waits once, at the end.
+
+The EOS stop (generate_tinyllama.py:770) is optional; fixed-length runs
+disable it.
+"""
+
+from __future__ import annotations
+
+import statistics
+import time
+from typing import Any, Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from .generation import verify_greedy_block_with_bonus
+from .lazy import get_compiler
+from .llama import (
+    LlamaConfig,
+    LlamaDecoderBlock,
+    LlamaDecoderStep,
+    LlamaForCausalLM,
+    _rope_rotations,
+    block_masks,
+    decode_masks,
+    position_selector,
+)
+from .tensor import Tensor, compile_graph, no_grad
+
+
+def sample_token(logits: np.ndarray, *, temperature: float, top_k: int, rng: np.random.Generator) -> int:
+    """Host sampling (generate_tinyllama.py:124-143): greedy at temperature
+    0, else softmax over the top-k logits scaled by 1/temperature."""
+    values = np.asarray(logits, dtype=np.float64).reshape(-1)
+    if temperature == 0:
+        return int(values.argmax())
+    values = values / temperature
+    if 0 < top_k < values.size:
+        keep = np.argpartition(values, -top_k)[-top_k:]
+        filtered = np.full_like(values, -np.inf)
+        filtered[keep] = values[keep]
+        values = filtered
+    values -= values.max()
+    probabilities = np.exp(values)
+    probabilities /= probabilities.sum()
+    return int(rng.choice(values.size, p=probabilities))
+
+
+def _host_float(values: np.ndarray) -> np.ndarray:
+    from .dtypes import BFLOAT16, bf16_to_float32
+    values = np.asarray(values)
+    return bf16_to_float32(values) if values.dtype == BFLOAT16 else values.astype(np.float32)
+
+
+class LlamaRuntime:
+    def __init__(self, config: LlamaConfig, weights: Dict[str, Tensor], *,
+                 compiler: str = "hip", dtype: Optional[object] = None) -> None:
+        self.config = config
+        self.weights = weights
+        self.compiler_name = compiler
+        self.compiler = get_compiler(compiler)
+        self.device = self.compiler.device
+        self.dtype = np.dtype(dtype if dtype is not None else getattr(self.device, "inference_dtype", np.float32))
+        self._prefill_programs: Dict[Tuple[int, int], Tuple[Any, Any]] = {}
+        self._decoder_programs: Dict[Tuple[int, bool], Tuple[Any, List[Any]]] = {}
+        self._block_programs: Dict[Tuple[int, int], Tuple[Any, List[Any]]] = {}
+
+    # -- prefill ----------------------------------------------------------------
+    def prefill(self, prompt: Sequence[int], context: int):
+        """Run (and cache) the prefill program: returns (logits, caches)."""
+        key = (len(prompt), context)
+        inputs = np.asarray(prompt, dtype=np.int32).reshape(1, -1)
+        cached = self._prefill_programs.get(key)
+        if cached is None:
+            model = LlamaForCausalLM(self.config, self.weights, sequence_length=len(prompt),
+                                     dtype=self.dtype, cache_length=context)
+            token_tensor = Tensor(inputs, copy=False)
+            selector = Tensor(position_selector(len(prompt) - 1, len(prompt), dtype=self.dtype), copy=False)
+            outputs = model.prefill(token_tensor, selector)
+            program = compile_graph(*outputs, compiler=self.compiler_name, dynamic_inputs=(token_tensor,))
+            self._prefill_programs[key] = (program, token_tensor._node)
+            bindings = None
+        else:
+            program, node = cached
+            bindings = {node: self.device.array(inputs)}
+        native = program.run(bindings, synchronize=False)
+        return native[0], list(native[1:])
+
+    # -- decode program -------------------------------------------------------------
+    def _decoder(self, context: int, position: int, caches: List[Any], *, donate: bool):
+        key = (context, donate)
+        cached = self._decoder_programs.get(key)
+        if cached is not None:
+            return cached
+        c = self.config
+        rotation = _rope_rotations(1, c.head_size, c.rope_theta, self.dtype, offset=position)
+        attention, write = decode_masks(position, context, self.dtype)
+        leaves = [
+            Tensor(np.zeros((1, 1), dtype=np.int32), copy=False),
+            Tensor(rotation, copy=False),
+            Tensor(attention, copy=False),
+            Tensor(write, copy=False),
+            Tensor(np.asarray(position, dtype=np.int32), copy=False),
+        ]
+        cache_tensors = [
+            Tensor.from_native(value, backend=self.device.name, shape=tuple(value.shape), dtype=self.dtype)
+            for value in caches
+        ]
+        decoder = LlamaDecoderStep(c, self.weights, cache_length=context, dtype=self.dtype)
+        outputs = decoder(*leaves[:4], list(zip(cache_tensors[::2], cache_tensors[1::2])), position=leaves[4])
+        dynamic = leaves + cache_tensors
+        kwargs = {}
+        if donate:
+            kwargs["donate"] = [t._node for t in cache_tensors]
+        program = self.compiler.compile([o._node for o in outputs], [t._node for t in dynamic], **kwargs)
+        entry = (program, [t._node for t in dynamic])
+        self._decoder_programs[key] = entry
+        return entry
+
+    # -- generation ------------------------------------------------------------------
+    def generate(
+        self,
+        prompt: Sequence[int],
+        max_new_tokens: int,
+        *,
+        temperature: float = 0.0,
+        top_k: int = 50,
+        seed: int = 0,
+        stop_at_eos: bool = False,
+        loop: Optional[str] = None,
+    ) -> Dict[str, object]:
+        if max_new_tokens <= 0:
+            raise ValueError("max_new_tokens must be positive")
+        if not len(prompt):
+            raise ValueError("the prompt produced no tokens")
+        context = len(prompt) + max_new_tokens
+        if context > self.config.max_position_embeddings:
+            raise ValueError(f"prompt plus output is {context} tokens, model limit is "
+                             f"{self.config.max_position_embeddings}")
+        if loop is None:
+            loop = "resident" if (self.compiler_name == "hip" and temperature == 0) else "reference"
+        if loop == "resident":
+            if temperature != 0:
+                raise ValueError("the resident loop is greedy only")
+            return self._generate_resident(prompt, max_new_tokens, context, stop_at_eos)
+        return self._generate_reference(prompt, max_new_tokens, context, temperature, top_k, seed, stop_at_eos)
+
+    def _generate_reference(self, prompt, max_new_tokens, context, temperature, top_k, seed, stop_at_eos):
+        rng = np.random.default_rng(seed)
+        device = self.device
+        tokens = [int(t) for t in prompt]
+        generated: List[int] = []
+        step_seconds: List[float] = []
+        started = time.perf_counter()
+        with no_grad():
+            step_started = time.perf_counter()
+            logits, caches = self.prefill(tokens, context)
+            token = self._sample(logits, temperature, top_k, rng)
+            step_seconds.append(time.perf_counter() - step_started)
+            tokens.append(token)
+            generated.append(token)
+            for _ in range(1, max_new_tokens):
+                if stop_at_eos and token == self.config.eos_token_id:
+                    break
+                position = len(tokens) - 1
+                c = self.config
+                rotation = _rope_rotations(1, c.head_size, c.rope_theta, self.dtype, offset=position)
+                attention, write = decode_masks(position, context, self.dtype)
+                step_started = time.perf_counter()
+                program, nodes = self._decoder(context, position, caches, donate=False)
+                values = [
+                    device.array(np.asarray([[token]], dtype=np.int32)),
+                    device.array(rotation),
+                    device.array(attention),
+                    device.array(write),
+                    device.array(np.asarray(position, dtype=np.int32)),
+                    *caches,
+                ]
+                native = program.run(dict(zip(nodes, values)), synchronize=False)
+                token = self._sample(native[0], temperature, top_k, rng)
+                step_seconds.append(time.perf_counter() - step_started)
+                tokens.append(token)
+                generated.append(token)
+                caches = list(native[1:])
+        warm = step_seconds[1:]
+        return {
+            "loop": "reference",
+            "generated_token_ids": generated,
+            "prompt_tokens": len(prompt),
+            "generated_tokens": len(generated),
+            "first_token_seconds": step_seconds[0],
+            "warm_token_median_seconds": statistics.median(warm) if warm else None,
+            "warm_tokens_per_second": 1 / statistics.median(warm) if warm else None,
+            "total_generation_seconds": sum(step_seconds),
+            "wall_generation_seconds": time.perf_counter() - started,
+            "fixed_context_tokens": context,
+            "kv_cache": True,
+        }
+
+    def _sample(self, logits, temperature, top_k, rng) -> int:
+        if temperature == 0:
+            return self.device.argmax(logits)
+        return sample_token(_host_float(self.device.to_numpy(logits)), temperature=temperature,
+                            top_k=top_k, rng=rng)
+
+    def _generate_resident(self, prompt, max_new_tokens, context, stop_at_eos):
+        device = self.device
+        started = time.perf_counter()
+        history = device.empty((max_new_tokens,), np.int32)
+        token = device.empty((1, 1), np.int32)
+        with no_grad():
+            first_started = time.perf_counter()
+            logits, caches = self.prefill(prompt, context)
+            device.greedy_advance(logits, token, history=history, step=0)
+            position_value = len(prompt)
+            attention_host, write_host = decode_masks(position_value, context, self.dtype)
+            position = device.array(np.asarray(position_value, dtype=np.int32))
+            attention = device.array(attention_host)
+            write = device.array(write_host)
+            device.synchronize()
+            first_token_seconds = time.perf_counter() - first_started
+            decode_started = time.perf_counter()
+            if max_new_tokens > 1:
+                program, nodes = self._decoder(context, position_value, caches, donate=True)
+                placeholder_rotation = device.array(_rope_rotations(
+                    1, self.config.head_size, self.config.rope_theta, self.dtype, offset=position_value))
+                bindings = dict(zip(nodes, [token, placeholder_rotation, attention, write, position, *caches]))
+                logits_out = device.empty(program._planned.output_nodes[0].shape, self.dtype)
+                outs = [logits_out]
+                for step in range(1, max_new_tokens):
+                    program.run(bindings, out=outs)
+                    device.greedy_advance(logits_out, token, history=history, step=step,
+                                          position=position, attention_mask=attention,
+                                          write_mask=write, cache_length=context)
+            device.synchronize()
+            decode_seconds = time.perf_counter() - decode_started
+        generated = [int(t) for t in device.to_numpy(history)]
+        if stop_at_eos and self.config.eos_token_id in generated:
+            generated = generated[: generated.index(self.config.eos_token_id) + 1]
+        decode_tokens = max_new_tokens - 1
+        return {
+            "loop": "resident",
+            "generated_token_ids": generated,
+            "prompt_tokens": len(prompt),
+            "generated_tokens": len(generated),
+            "first_token_seconds": first_token_seconds,
+            "decode_seconds": decode_seconds,
+            "warm_token_median_seconds": decode_seconds / decode_tokens if decode_tokens else None,
+            "warm_tokens_per_second": decode_tokens / decode_seconds if decode_tokens else None,
+            "wall_generation_seconds": time.perf_counter() - started,
+            "fixed_context_tokens": context,
+            "kv_cache": True,
+        }

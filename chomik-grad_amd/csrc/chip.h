@@ -1,0 +1,176 @@
+// Internal header of libchomik_hip: dtype helpers, the uniform kernel
+// argument block and the kernel registry shared by every .hip file.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace chip {
+
+enum DType : int { F32 = 0, F16 = 1, BF16 = 2, I32 = 3, I64 = 4 };
+
+inline size_t dtype_size(int dt) {
+  switch (dt) {
+    case F32: return 4;
+    case F16: return 2;
+    case BF16: return 2;
+    case I32: return 4;
+    case I64: return 8;
+    default: return 0;
+  }
+}
+
+// Every kernel takes one KArgs by value.  p[] are device pointers resolved
+// from plan slots; n[] integer parameters; f[] float parameters.  Each kernel
+// documents its own layout next to its definition.
+constexpr int kMaxPtr = 16;
+constexpr int kMaxInt = 112;
+constexpr int kMaxFloat = 8;
+struct KArgs {
+  void* p[kMaxPtr];
+  int64_t n[kMaxInt];
+  float f[kMaxFloat];
+};
+
+// Error bits OR-ed into the library's device error word by kernels.
+enum ErrorBit : int {
+  ERR_GATHER_INDEX = 1,   // gather index outside the table
+  ERR_POSITION = 2,       // RoPE / KV position outside its table or cache
+  ERR_SHAPE = 4,          // a runtime shape check inside a kernel failed
+};
+
+// Planners of kernels that can raise an error bit put the library's device
+// error word in p[kErrPtr]; tapes never address that entry.
+constexpr int kErrPtr = kMaxPtr - 1;
+__device__ __forceinline__ void raise_error(const KArgs& a, int bit) {
+  atomicOr(static_cast<int*>(a.p[kErrPtr]), bit);
+}
+
+// ---------------------------------------------------------------- device
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t bits) {
+  return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+// float32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float value) {
+  uint32_t u = __float_as_uint(value);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_f16(float v) { return __half2float(__float2half(v)); }
+__device__ __forceinline__ float round_bf16(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// Round a float32 intermediate to the storage precision of ``dt`` (the
+// rounding a NumPy float16 ufunc applies after every operation).
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == F16) return round_f16(v);
+  if (dt == BF16) return round_bf16(v);
+  return v;
+}
+
+__device__ __forceinline__ float load_f(const void* base, int64_t i, int dt) {
+  switch (dt) {
+    case F32: return static_cast<const float*>(base)[i];
+    case F16: return __half2float(static_cast<const __half*>(base)[i]);
+    case BF16: return bf16_bits_to_f32(static_cast<const uint16_t*>(base)[i]);
+    case I32: return static_cast<float>(static_cast<const int32_t*>(base)[i]);
+    case I64: return static_cast<float>(static_cast<const int64_t*>(base)[i]);
+  }
+  return 0.f;
+}
+
+__device__ __forceinline__ void store_f(void* base, int64_t i, int dt, float v) {
+  switch (dt) {
+    case F32: static_cast<float*>(base)[i] = v; break;
+    case F16: static_cast<__half*>(base)[i] = __float2half(v); break;
+    case BF16: static_cast<uint16_t*>(base)[i] = f32_to_bf16_bits(v); break;
+    default: break;
+  }
+}
+
+// Typed element access for templated kernels.
+struct bf16_t { uint16_t bits; };
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int code = F32;
+  __device__ static __forceinline__ float to_f(float v) { return v; }
+  __device__ static __forceinline__ float from_f(float v) { return v; }
+  __device__ static __forceinline__ float round(float v) { return v; }
+};
+template <> struct Elem<__half> {
+  static constexpr int code = F16;
+  __device__ static __forceinline__ float to_f(__half v) { return __half2float(v); }
+  __device__ static __forceinline__ __half from_f(float v) { return __float2half(v); }
+  __device__ static __forceinline__ float round(float v) { return round_f16(v); }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int code = BF16;
+  __device__ static __forceinline__ float to_f(bf16_t v) { return bf16_bits_to_f32(v.bits); }
+  __device__ static __forceinline__ bf16_t from_f(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+  __device__ static __forceinline__ float round(float v) { return round_bf16(v); }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Sum over a 256-thread block (4 waves); every thread gets the result.
+__device__ __forceinline__ float block_sum256(float v, float* scratch4) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) scratch4[wave] = v;
+  __syncthreads();
+  return (scratch4[0] + scratch4[1]) + (scratch4[2] + scratch4[3]);
+}
+__device__ __forceinline__ float block_max256(float v, float* scratch4) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) scratch4[wave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(scratch4[0], scratch4[1]), fmaxf(scratch4[2], scratch4[3]));
+}
+
+// ---------------------------------------------------------------- host
+// A launch decided by a kernel's planner: which function, with what shape.
+struct Launch {
+  const void* func = nullptr;
+  dim3 grid{1, 1, 1};
+  dim3 block{1, 1, 1};
+  size_t shmem = 0;
+};
+
+// Each step kind has a planner that validates KArgs and fills a Launch.
+// Returns 0 or an error message (static string).
+using Planner = const char* (*)(KArgs& a, Launch& l);
+
+void register_kind(int kind, Planner planner);
+Planner planner_for(int kind);
+
+// The library's device error word (device pointer), defined in runtime.hip.
+int* device_error_word();
+// Record an error message for chip_last_error(); returns ``code``.
+int set_error(int code, const char* message);
+
+}  // namespace chip
+
+// Registration helper: CHIP_KIND(7, plan_fn) at namespace scope.
+#define CHIP_REGISTER_KIND(kind, fn)                                   \
+  static const int chip_reg_##fn = ([] {                               \
+    ::chip::register_kind((kind), (fn));                               \
+    return 0;                                                          \
+  })()

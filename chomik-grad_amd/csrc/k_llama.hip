@@ -1,0 +1,422 @@
+// Kernels for the Llama lowerings: rms_norm, rope, sdpa, the KV-cache write
+// and placement patterns, argmax and device-side greedy feedback.
+//
+// Each fused kernel reproduces the rounding points of the portable graph it
+// replaces (chomikgrad/llama.py): for float16/bfloat16 every elementwise step
+// is rounded to the storage type and every contraction accumulates in
+// float32 and rounds once, as NumPy's half loops do.  For float32 the
+// roundings are no-ops.
+#include "chip.h"
+#include "chomik_hip.h"
+
+namespace chip {
+namespace {
+
+// ---------------------------------------------------------------- rmsnorm
+// y = x / sqrt(mean(x * x) + eps) * w   (llama.py _rms_norm)
+// p[0] x, p[1] w, p[2] out; n[0] rows, n[1] D, n[2] x row stride, n[3] dtype,
+// n[4] weight dtype; f[0] eps.  One 256-thread block per row.
+__global__ __launch_bounds__(256) void k_rmsnorm(KArgs a) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t D = a.n[1];
+  const int dt = static_cast<int>(a.n[3]), wdt = static_cast<int>(a.n[4]);
+  const int64_t xb = row * a.n[2];
+  float ss = 0.f;
+  for (int64_t k = threadIdx.x; k < D; k += 256) {
+    const float x = load_f(a.p[0], xb + k, dt);
+    ss += round_to(x * x, dt);
+  }
+  ss = round_to(block_sum256(ss, red), dt);
+  const float mean = round_to(ss / round_to(static_cast<float>(D), dt), dt);
+  const float var = round_to(mean + round_to(a.f[0], dt), dt);
+  const float r = round_to(sqrtf(var), dt);
+  for (int64_t k = threadIdx.x; k < D; k += 256) {
+    const float x = load_f(a.p[0], xb + k, dt);
+    const float y = round_to(round_to(x / r, dt) * load_f(a.p[1], k, wdt), dt);
+    store_f(a.p[2], row * D + k, dt, y);
+  }
+}
+
+const char* plan_rmsnorm(KArgs& a, Launch& l) {
+  if (a.n[0] < 0 || a.n[1] <= 0) return "rmsnorm: bad sizes";
+  if (a.n[0] > 2147483647) return "rmsnorm: too many rows";
+  l.func = reinterpret_cast<const void*>(&k_rmsnorm);
+  l.grid = dim3(static_cast<unsigned>(a.n[0] > 0 ? a.n[0] : 1));
+  l.block = dim3(256);
+  return nullptr;
+}
+
+// ---------------------------------------------------------------- rope
+// Rotate-half RoPE with a cos/sin table of the model dtype (the values the
+// portable rotation matrix holds).  For pair (i, i + h):
+//   out[i]     = x[i] * cos_i - x[i + h] * sin_i
+//   out[i + h] = x[i] * sin_i + x[i + h] * cos_i
+// (two exact half-precision products summed in float32, rounded once: the
+// row-vector x rotation-matrix product of llama.py _rotate).
+// p[0] x, p[1] positions (int32 or null), p[2] table (len, 2, h), p[3] out.
+// n[0] B, n[1] H, n[2] T, n[3] hd, n[4..7] x strides (b, h, t, d), n[8]
+// dtype, n[9] mode (0: offset + t, 1: scalar position + offset + t,
+// 2: position[b] + offset + t), n[10] offset, n[11] table length.
+__global__ void k_rope(KArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t B = a.n[0], H = a.n[1], T = a.n[2], hd = a.n[3];
+  if (row >= B * H * T) return;
+  const int64_t t = row % T, h = (row / T) % H, b = row / (T * H);
+  const int dt = static_cast<int>(a.n[8]);
+  int64_t pos = a.n[10] + t;
+  if (a.n[9] == 1) pos += static_cast<const int32_t*>(a.p[1])[0];
+  if (a.n[9] == 2) pos += static_cast<const int32_t*>(a.p[1])[b];
+  const int64_t half = hd / 2;
+  const int64_t xb = b * a.n[4] + h * a.n[5] + t * a.n[6];
+  const bool ok = pos >= 0 && pos < a.n[11];
+  if (!ok && lane == 0) raise_error(a, ERR_POSITION);
+  for (int64_t i = lane; i < half; i += 64) {
+    float o1 = 0.f, o2 = 0.f;
+    if (ok) {
+      const float x1 = load_f(a.p[0], xb + i * a.n[7], dt);
+      const float x2 = load_f(a.p[0], xb + (i + half) * a.n[7], dt);
+      const float c = load_f(a.p[2], pos * hd + i, dt);
+      const float s = load_f(a.p[2], pos * hd + half + i, dt);
+      o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x2, -s));
+      o2 = __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c));
+    }
+    store_f(a.p[3], row * hd + i, dt, o1);
+    store_f(a.p[3], row * hd + half + i, dt, o2);
+  }
+}
+
+const char* plan_rope(KArgs& a, Launch& l) {
+  if (a.n[0] <= 0 || a.n[1] <= 0 || a.n[2] <= 0 || a.n[3] <= 0 || (a.n[3] & 1)) return "rope: bad shape";
+  if (a.n[9] < 0 || a.n[9] > 2) return "rope: bad position mode";
+  const int64_t rows = a.n[0] * a.n[1] * a.n[2];
+  l.func = reinterpret_cast<const void*>(&k_rope);
+  l.grid = dim3(static_cast<unsigned>((rows + 3) / 4));
+  l.block = dim3(256);
+  a.p[kErrPtr] = device_error_word();
+  return nullptr;
+}
+
+// ---------------------------------------------------------------- sdpa
+// softmax(q K^T / d + mask) V for GQA (query head h reads KV head
+// h / (H / KV)), with the portable graph's rounding points:
+//   s = round(round(round(q.k) / d) + mask)      (d = round(sqrt(hd)))
+//   e = round(exp(round(s - max s)));  S = round(sum e)
+//   out = round(sum_j round(e_j / S) * v_j)
+// p[0] q, p[1] K, p[2] V, p[3] mask (or null), p[4] out (B, H, T, hd).
+// n[0] B, n[1] H, n[2] T, n[3] C, n[4] hd, n[5] KV, n[6] dtype, n[7..10] q
+// strides (b, h, t, d), n[11..14] K strides (b, kv, c, d), n[15..18] V
+// strides, n[19..22] mask strides (b, h, t, c), n[23] mask dtype; f[0] d.
+// One 256-thread block per (b, h, t); scores live in dynamic LDS.
+__global__ __launch_bounds__(256) void k_sdpa(KArgs a) {
+  extern __shared__ float lds[];
+  __shared__ float red[4];
+  __shared__ float qrow[256];
+  const int64_t B = a.n[0], H = a.n[1], T = a.n[2], C = a.n[3], hd = a.n[4], KV = a.n[5];
+  const int64_t row = blockIdx.x;
+  const int64_t t = row % T, h = (row / T) % H, b = row / (T * H);
+  const int64_t g = h / (H / KV);
+  const int dt = static_cast<int>(a.n[6]);
+  (void)B;
+  float* scores = lds;                 // C floats
+  float* partial = lds + C;            // 4 x hd floats
+  for (int64_t d = threadIdx.x; d < hd; d += 256)
+    qrow[d] = load_f(a.p[0], b * a.n[7] + h * a.n[8] + t * a.n[9] + d * a.n[10], dt);
+  __syncthreads();
+  const float div = round_to(a.f[0], dt);
+  const int64_t kb = b * a.n[11] + g * a.n[12];
+  const int64_t mb = b * a.n[19] + h * a.n[20] + t * a.n[21];
+  float local_max = -INFINITY;
+  for (int64_t j = threadIdx.x; j < C; j += 256) {
+    float dot = 0.f;
+    const int64_t kr = kb + j * a.n[13];
+    for (int64_t d = 0; d < hd; ++d) dot += qrow[d] * load_f(a.p[1], kr + d * a.n[14], dt);
+    float s = round_to(round_to(dot, dt) / div, dt);
+    if (a.p[3]) s = round_to(s + load_f(a.p[3], mb + j * a.n[22], static_cast<int>(a.n[23])), dt);
+    scores[j] = s;
+    local_max = (s != s || s > local_max) ? s : local_max;
+  }
+  const float m = block_max256(local_max, red);
+  float local_sum = 0.f;
+  for (int64_t j = threadIdx.x; j < C; j += 256) {
+    const float e = round_to(expf(round_to(scores[j] - m, dt)), dt);
+    scores[j] = e;
+    local_sum += e;
+  }
+  const float S = round_to(block_sum256(local_sum, red), dt);
+  const int lane = threadIdx.x & 63, group = threadIdx.x >> 6;
+  const int64_t vb = b * a.n[15] + g * a.n[16];
+  for (int64_t d0 = 0; d0 < hd; d0 += 64) {
+    const int64_t d = d0 + lane;
+    float acc = 0.f;
+    if (d < hd)
+      for (int64_t j = group; j < C; j += 4)
+        acc += round_to(scores[j] / S, dt) * load_f(a.p[2], vb + j * a.n[17] + d * a.n[18], dt);
+    __syncthreads();
+    if (d < hd) partial[group * 64 + lane] = acc;
+    __syncthreads();
+    if (group == 0 && d < hd) {
+      const float total = (partial[lane] + partial[64 + lane]) + (partial[128 + lane] + partial[192 + lane]);
+      store_f(a.p[4], row * hd + d, dt, total);
+    }
+  }
+}
+
+const char* plan_sdpa(KArgs& a, Launch& l) {
+  for (int i = 0; i < 6; ++i)
+    if (a.n[i] <= 0) return "sdpa: empty dimension";
+  if (a.n[1] % a.n[5]) return "sdpa: heads not divisible by KV heads";
+  if (a.n[4] > 256) return "sdpa: head size above 256";
+  if (a.n[3] > 32768) return "sdpa: more than 32768 keys for the generic kernel";
+  const int64_t rows = a.n[0] * a.n[1] * a.n[2];
+  if (rows > 2147483647) return "sdpa: too many rows";
+  l.func = reinterpret_cast<const void*>(&k_sdpa);
+  l.grid = dim3(static_cast<unsigned>(rows));
+  l.block = dim3(256);
+  l.shmem = static_cast<size_t>(a.n[3] + 4 * 64) * sizeof(float);
+  if (l.shmem > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_sdpa),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(l.shmem)) != hipSuccess)
+    return "sdpa: cannot raise the LDS limit";
+  return nullptr;
+}
+
+// ---------------------------------------------------------------- kv write
+// new = cache * (1 - w) + x * w   (llama.py decode cache update), rounded as
+// round(round(c * round(1 - w)) + round(x * w)).  w is per (b, row); x is the
+// new row(s) broadcast along the cache rows.  In place (out == cache), only
+// rows with w != 0 are touched: for the others the formula returns the
+// cache value itself (up to the sign of a zero).
+// p[0] cache, p[1] x, p[2] w, p[3] out.
+// n[0] B, n[1] KV, n[2] C, n[3] hd, n[4] dtype, n[5..8] x strides (b, kv,
+// row, d), n[9] w b-stride, n[10] w row-stride, n[11] in place, n[12..15]
+// cache strides (b, kv, row, d), n[16] w dtype.
+__device__ __forceinline__ float kv_blend(float c, float x, float w, int dt) {
+  return round_to(round_to(c * round_to(1.f - w, dt), dt) + round_to(x * w, dt), dt);
+}
+
+__global__ void k_kv_write_inplace(KArgs a) {
+  // grid (B * KV); each thread scans rows.
+  const int64_t KV = a.n[1], C = a.n[2], hd = a.n[3];
+  const int64_t b = blockIdx.x / KV, g = blockIdx.x % KV;
+  const int dt = static_cast<int>(a.n[4]), wdt = static_cast<int>(a.n[16]);
+  for (int64_t r = threadIdx.x; r < C; r += blockDim.x) {
+    const float w = load_f(a.p[2], b * a.n[9] + r * a.n[10], wdt);
+    if (w == 0.f) continue;
+    const int64_t cb = b * a.n[12] + g * a.n[13] + r * a.n[14];
+    const int64_t xb = b * a.n[5] + g * a.n[6] + r * a.n[7];
+    for (int64_t d = 0; d < hd; ++d) {
+      const float c = load_f(a.p[0], cb + d * a.n[15], dt);
+      const float x = load_f(a.p[1], xb + d * a.n[8], dt);
+      store_f(a.p[3], cb + d * a.n[15], dt, kv_blend(c, x, w, dt));
+    }
+  }
+}
+
+__global__ void k_kv_write_copy(KArgs a) {
+  // one wavefront per cache row; out contiguous (B, KV, C, hd)
+  const int lane = threadIdx.x & 63;
+  const int64_t KV = a.n[1], C = a.n[2], hd = a.n[3];
+  const int64_t row = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= a.n[0] * KV * C) return;
+  const int64_t r = row % C, g = (row / C) % KV, b = row / (C * KV);
+  const int dt = static_cast<int>(a.n[4]), wdt = static_cast<int>(a.n[16]);
+  const float w = load_f(a.p[2], b * a.n[9] + r * a.n[10], wdt);
+  const int64_t cb = b * a.n[12] + g * a.n[13] + r * a.n[14];
+  const int64_t xb = b * a.n[5] + g * a.n[6] + r * a.n[7];
+  for (int64_t d = lane; d < hd; d += 64) {
+    const float c = load_f(a.p[0], cb + d * a.n[15], dt);
+    const float x = load_f(a.p[1], xb + d * a.n[8], dt);
+    store_f(a.p[3], row * hd + d, dt, kv_blend(c, x, w, dt));
+  }
+}
+
+const char* plan_kv_write(KArgs& a, Launch& l) {
+  for (int i = 0; i < 4; ++i)
+    if (a.n[i] <= 0) return "kv_write: empty dimension";
+  if (a.n[11]) {
+    l.func = reinterpret_cast<const void*>(&k_kv_write_inplace);
+    l.grid = dim3(static_cast<unsigned>(a.n[0] * a.n[1]));
+    l.block = dim3(256);
+  } else {
+    const int64_t rows = a.n[0] * a.n[1] * a.n[2];
+    l.func = reinterpret_cast<const void*>(&k_kv_write_copy);
+    l.grid = dim3(static_cast<unsigned>((rows + 3) / 4));
+    l.block = dim3(256);
+  }
+  return nullptr;
+}
+
+// ---------------------------------------------------------------- kv place
+// new = cache * (1 - w) + (x^T @ placement)^T   (llama.py block update):
+// row r of the placed term is round(sum_t placement[t, r] * x[t]) (float32
+// accumulation), then blended as round(round(c * round(1 - w)) + placed).
+// In place, rows with w == 0 and an all-zero placement column are skipped.
+// p[0] cache, p[1] x, p[2] placement, p[3] w, p[4] out.
+// n[0] B, n[1] KV, n[2] C, n[3] hd, n[4] dtype, n[5] T, n[6..9] x strides
+// (b, kv, t, d), n[10..11] placement strides (t, row), n[12..13] w strides
+// (b, row), n[14] in place, n[15..18] cache strides, n[19] placement dtype,
+// n[20] w dtype.
+__global__ void k_kv_place(KArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t KV = a.n[1], C = a.n[2], hd = a.n[3], T = a.n[5];
+  const int64_t row = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= a.n[0] * KV * C) return;
+  const int64_t r = row % C, g = (row / C) % KV, b = row / (C * KV);
+  const int dt = static_cast<int>(a.n[4]);
+  const int pdt = static_cast<int>(a.n[19]), wdt = static_cast<int>(a.n[20]);
+  const float w = load_f(a.p[3], b * a.n[12] + r * a.n[13], wdt);
+  bool touched = w != 0.f;
+  for (int64_t t = 0; t < T && !touched; ++t)
+    touched = load_f(a.p[2], t * a.n[10] + r * a.n[11], pdt) != 0.f;
+  const bool in_place = a.n[14] != 0;
+  if (in_place && !touched) return;
+  const int64_t cb = b * a.n[15] + g * a.n[16] + r * a.n[17];
+  const int64_t ob = in_place ? cb : row * hd;
+  const int64_t od = in_place ? a.n[18] : 1;
+  for (int64_t d = lane; d < hd; d += 64) {
+    float placed = 0.f;
+    for (int64_t t = 0; t < T; ++t)
+      placed += load_f(a.p[1], b * a.n[6] + g * a.n[7] + t * a.n[8] + d * a.n[9], dt) *
+                load_f(a.p[2], t * a.n[10] + r * a.n[11], pdt);
+    const float c = load_f(a.p[0], cb + d * a.n[18], dt);
+    const float kept = round_to(c * round_to(1.f - w, dt), dt);
+    store_f(a.p[4], ob + d * od, dt, round_to(kept + round_to(placed, dt), dt));
+  }
+}
+
+const char* plan_kv_place(KArgs& a, Launch& l) {
+  for (int i = 0; i < 4; ++i)
+    if (a.n[i] <= 0) return "kv_place: empty dimension";
+  if (a.n[5] <= 0) return "kv_place: empty block";
+  const int64_t rows = a.n[0] * a.n[1] * a.n[2];
+  l.func = reinterpret_cast<const void*>(&k_kv_place);
+  l.grid = dim3(static_cast<unsigned>((rows + 3) / 4));
+  l.block = dim3(256);
+  return nullptr;
+}
+
+// ---------------------------------------------------------------- argmax
+// First index of the maximum; NaN counts as the maximum (NumPy argmax).
+struct Best {
+  float v;
+  int64_t i;
+};
+__device__ __forceinline__ Best better(Best x, Best y) {
+  const bool xn = x.v != x.v, yn = y.v != y.v;
+  if (xn || yn) {
+    if (xn && yn) return x.i <= y.i ? x : y;
+    return xn ? x : y;
+  }
+  if (x.v > y.v) return x;
+  if (y.v > x.v) return y;
+  return x.i <= y.i ? x : y;
+}
+
+__device__ Best row_argmax(const void* src, int dt, int64_t row, int64_t cols) {
+  __shared__ float sv[16];
+  __shared__ int64_t si[16];
+  Best best{-INFINITY, cols};
+  for (int64_t j = threadIdx.x; j < cols; j += blockDim.x)
+    best = better(best, Best{load_f(src, row * cols + j, dt), j});
+  if (best.i == cols) best.i = INT64_MAX;  // no element seen by this thread
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    Best other{__shfl_xor(best.v, o, 64), __shfl_xor(best.i, o, 64)};
+    best = better(best, other);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) {
+    sv[wave] = best.v;
+    si[wave] = best.i;
+  }
+  __syncthreads();
+  Best total{sv[0], si[0]};
+  for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) total = better(total, Best{sv[w], si[w]});
+  return total;
+}
+
+__global__ __launch_bounds__(1024) void k_argmax(const void* src, int dt, int64_t cols, int64_t* out) {
+  const Best best = row_argmax(src, dt, blockIdx.x, cols);
+  if (threadIdx.x == 0) out[blockIdx.x] = best.i;
+}
+
+struct Advance {
+  const void* logits;
+  int logits_dtype;
+  int mask_dtype;
+  int64_t cols;
+  int32_t* tokens;
+  int32_t* history;
+  int64_t step;
+  int32_t* position;
+  void* attention;
+  int64_t mask_row;
+  void* write;
+  int64_t write_row;
+  int64_t cache_length;
+  int64_t rows;
+  int* error;
+};
+
+__global__ __launch_bounds__(1024) void k_greedy_advance(Advance a) {
+  const int64_t row = blockIdx.x;
+  const Best best = row_argmax(a.logits, a.logits_dtype, row, a.cols);
+  if (threadIdx.x != 0) return;
+  const int32_t token = static_cast<int32_t>(best.i);
+  a.tokens[row] = token;
+  if (a.history) a.history[a.step * a.rows + row] = token;
+  if (!a.position) return;
+  const int64_t next = static_cast<int64_t>(a.position[row]) + 1;
+  if (next >= a.cache_length) {
+    atomicOr(a.error, ERR_POSITION);
+    return;
+  }
+  a.position[row] = static_cast<int32_t>(next);
+  if (a.attention) store_f(a.attention, row * a.mask_row + next, a.mask_dtype, 0.f);
+  if (a.write) {
+    store_f(a.write, row * a.write_row + next - 1, a.mask_dtype, 0.f);
+    store_f(a.write, row * a.write_row + next, a.mask_dtype, 1.f);
+  }
+}
+
+}  // namespace
+
+int launch_argmax(const void* src, int dtype, int64_t rows, int64_t cols, int64_t* out_dev,
+                  hipStream_t stream) {
+  if (dtype != F32 && dtype != F16 && dtype != BF16) return set_error(CHIP_EINVAL, "argmax: float dtype required");
+  if (rows > 2147483647) return set_error(CHIP_EINVAL, "argmax: too many rows");
+  hipLaunchKernelGGL(k_argmax, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, stream, src, dtype,
+                     cols, out_dev);
+  if (hipGetLastError() != hipSuccess) return set_error(CHIP_EHIP, "argmax launch failed");
+  return CHIP_OK;
+}
+
+int launch_greedy_advance(const void* logits, int logits_dtype, int64_t rows, int64_t cols,
+                          void* tokens_out, void* history, int64_t step, void* position,
+                          void* attention_mask, int64_t mask_row, void* write_mask,
+                          int64_t write_row, int mask_dtype, int64_t cache_length,
+                          hipStream_t stream) {
+  if (logits_dtype != F32 && logits_dtype != F16 && logits_dtype != BF16)
+    return set_error(CHIP_EINVAL, "greedy advance: float logits required");
+  if ((attention_mask || write_mask) && mask_dtype != F32 && mask_dtype != F16 && mask_dtype != BF16)
+    return set_error(CHIP_EINVAL, "greedy advance: float masks required");
+  Advance a{logits, logits_dtype, mask_dtype, cols, static_cast<int32_t*>(tokens_out),
+            static_cast<int32_t*>(history), step, static_cast<int32_t*>(position),
+            attention_mask, mask_row, write_mask, write_row, cache_length, rows,
+            device_error_word()};
+  hipLaunchKernelGGL(k_greedy_advance, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, stream, a);
+  if (hipGetLastError() != hipSuccess) return set_error(CHIP_EHIP, "greedy advance launch failed");
+  return CHIP_OK;
+}
+
+CHIP_REGISTER_KIND(CHIP_K_RMSNORM, plan_rmsnorm);
+CHIP_REGISTER_KIND(CHIP_K_ROPE, plan_rope);
+CHIP_REGISTER_KIND(CHIP_K_SDPA, plan_sdpa);
+CHIP_REGISTER_KIND(CHIP_K_KV_WRITE, plan_kv_write);
+CHIP_REGISTER_KIND(CHIP_K_KV_PLACE, plan_kv_place);
+
+}  // namespace chip

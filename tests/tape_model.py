@@ -1,0 +1,425 @@
+"""Host model of a plan tape -- TEST INFRASTRUCTURE ONLY.
+
+Decodes the int64 tape that ``chomikgrad._planner`` emits for
+``chip_plan_create`` and executes each step with NumPy, following the kernel
+semantics documented in chomik-grad_amd/csrc/*.hip (same parameter layout,
+same rounding points).  It lets CPU tests check the planner's lowering,
+fusion, memory plan and tape encoding against the oracle without a GPU.  It
+is never used by the product.
+
+``CpuPlanCompiler`` is a ``HIPCompiler`` whose device hands out host arrays
+with fake device addresses, so ``plan_graph`` runs unchanged.
+"""
+
+from __future__ import annotations
+
+import itertools
+from typing import Dict, List
+
+import numpy as np
+
+from chomikgrad import _planner as P
+from chomikgrad.dtypes import BFLOAT16
+from chomikgrad.hip_backend import HIPCompiler
+
+_addresses = itertools.count(1 << 24, 1 << 12)
+
+DT = {0: np.dtype(np.float32), 1: np.dtype(np.float16), 2: np.dtype(np.uint16),
+      3: np.dtype(np.int32), 4: np.dtype(np.int64)}
+
+
+class HostArray:
+    def __init__(self, host: np.ndarray):
+        self.host = np.ascontiguousarray(host)
+        self.shape = self.host.shape
+        self.dtype = self.host.dtype
+        self.nbytes = self.host.nbytes
+        self.ptr = next(_addresses)
+
+
+class HostDevice:
+    name = "hip"
+
+    def array(self, value):
+        return value if isinstance(value, HostArray) else HostArray(np.asarray(value))
+
+
+class CpuPlanCompiler(HIPCompiler):
+    def __init__(self):  # no library, no GPU
+        self.device = HostDevice()
+        self._rope_tables = {}
+        self._program_cache = {}
+
+
+def _round(values: np.ndarray, code: int) -> np.ndarray:
+    values = np.asarray(values, dtype=np.float32)
+    if code == 1:
+        return values.astype(np.float16).astype(np.float32)
+    if code == 2:
+        return _bf16_to_f32(_f32_to_bf16(values))
+    return values
+
+
+def _f32_to_bf16(values: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(values)
+    return np.where(nan, np.uint16(0x7FC0), rounded)
+
+
+def _bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint32) << 16).view(np.float32)
+
+
+class Memory:
+    def __init__(self, planned: P.PlannedProgram, inputs: Dict, outputs: Dict):
+        self.slots: Dict[int, np.ndarray] = {0: np.zeros(max(planned.arena_bytes, 16), np.uint8)}
+        for storage in planned.storages:
+            if storage.slot <= 0:
+                continue
+            if storage.kind == "const":
+                self.slots[storage.slot] = storage.native.host.view(np.uint8).reshape(-1).copy()
+            elif storage.kind == "input":
+                self.slots[storage.slot] = inputs[storage.leaf]
+            elif storage.kind == "output":
+                self.slots[storage.slot] = outputs[id(storage)]
+
+    def view(self, ptr, code, count) -> np.ndarray:
+        slot, offset = ptr
+        buffer = self.slots[slot]
+        dtype = DT[code]
+        return np.ndarray((count,), dtype=dtype, buffer=buffer, offset=offset)
+
+    def flat(self, ptr, code) -> np.ndarray:
+        slot, offset = ptr
+        buffer = self.slots[slot]
+        dtype = DT[code]
+        return np.ndarray(((buffer.size - offset) // dtype.itemsize,), dtype=dtype, buffer=buffer, offset=offset)
+
+
+def load(mem: Memory, ptr, code, index) -> np.ndarray:
+    data = mem.flat(ptr, code)[np.asarray(index, dtype=np.int64)]
+    if code == 2:
+        return _bf16_to_f32(data)
+    return data.astype(np.float32)
+
+
+def store(mem: Memory, ptr, code, index, values) -> None:
+    target = mem.flat(ptr, code)
+    values = np.asarray(values, dtype=np.float32)
+    if code == 2:
+        target[np.asarray(index, dtype=np.int64)] = _f32_to_bf16(values)
+    else:
+        target[np.asarray(index, dtype=np.int64)] = values.astype(DT[code])
+
+
+def strided_index(sizes, strides) -> np.ndarray:
+    index = np.zeros([int(s) for s in sizes], dtype=np.int64)
+    for d, (size, stride) in enumerate(zip(sizes, strides)):
+        shape = [1] * len(sizes)
+        shape[d] = int(size)
+        index = index + np.arange(int(size), dtype=np.int64).reshape(shape) * int(stride)
+    return index.reshape(-1) if len(sizes) else np.zeros(1, dtype=np.int64)
+
+
+def decode(tape: np.ndarray):
+    words = [int(w) for w in tape]
+    assert words[0] == 0x43484950 and words[1] == 1
+    n_steps = words[3]
+    at = 5
+    steps = []
+    for _ in range(n_steps):
+        kind, n_ptr, n_int, n_float = words[at:at + 4]
+        at += 4
+        ptrs = [(words[at + 2 * i], words[at + 2 * i + 1]) for i in range(n_ptr)]
+        at += 2 * n_ptr
+        ints = words[at:at + n_int]
+        at += n_int
+        floats = [float(np.array([w], dtype=np.uint32).view(np.float32)[0]) for w in words[at:at + n_float]]
+        at += n_float
+        steps.append((kind, ptrs, ints, floats))
+    assert at == len(words)
+    return steps
+
+
+def run(planned: P.PlannedProgram, leaf_values: Dict) -> List[np.ndarray]:
+    """Execute ``planned`` with host values for its input leaves."""
+    inputs = {}
+    for leaf, slot in planned.input_slots.items():
+        value = np.asarray(leaf_values[leaf])
+        if value.dtype == BFLOAT16:
+            value = value.view(np.uint16)
+        inputs[leaf] = np.ascontiguousarray(value).view(np.uint8).reshape(-1).copy()
+    outputs = {}
+    for kind, payload in planned.output_specs:
+        if kind == "output" and id(payload) not in outputs:
+            outputs[id(payload)] = np.zeros(max(payload.nbytes, 1), np.uint8)
+    mem = Memory(planned, inputs, outputs)
+    errors = 0
+    for kind, ptrs, n, f in decode(planned.tape):
+        errors |= STEP[kind](mem, ptrs, n, f)
+    if errors:
+        raise IndexError(f"kernel error bits {errors}")
+    results = []
+    for index, (kind, payload) in enumerate(planned.output_specs):
+        node = planned.output_nodes[index]
+        if kind == "output":
+            raw = outputs[id(payload)][: payload.nbytes]
+        elif kind == "input":
+            raw = inputs[payload] if payload in inputs else np.ascontiguousarray(
+                np.asarray(leaf_values[payload])).view(np.uint8).reshape(-1)
+        elif kind == "const":
+            raw = payload.host.view(np.uint8).reshape(-1)
+        else:
+            results.append(np.zeros(node.shape, node.dtype))
+            continue
+        dtype = np.dtype(np.uint16) if node.dtype == BFLOAT16 else node.dtype
+        value = raw.view(dtype).reshape(node.shape).copy()
+        results.append(value.view(BFLOAT16) if node.dtype == BFLOAT16 else value)
+    return results
+
+
+# ---------------------------------------------------------------- steps
+def s_fill(mem, p, n, f):
+    mem.view(p[0], 3, n[0])[:] = n[1]
+    return 0
+
+
+def s_copy(mem, p, n, f):
+    count, nd = n[0], n[1]
+    size = n[18]
+    index = strided_index(n[2:2 + nd], n[10:10 + nd])
+    if size == 1:
+        src = mem.slots[p[0][0]][p[0][1]:]
+        mem.slots[p[1][0]][p[1][1]:p[1][1] + count] = src[index]
+        return 0
+    code = {2: 2, 4: 3, 8: 4}[size]
+    mem.flat(p[1], code)[:count] = mem.flat(p[0], code)[index]
+    return 0
+
+
+def s_elementwise(mem, p, n, f):
+    count, nd = n[0], n[1]
+    sizes = n[2:2 + nd]
+    n_in, n_ops, out_dt = n[10], n[11], n[12]
+    regs = []
+    for k in range(n_in):
+        strides = n[19 + 8 * k: 19 + 8 * k + nd]
+        regs.append(load(mem, p[1 + k], n[13 + k], strided_index(sizes, strides)))
+    with np.errstate(all="ignore"):
+        for o in range(n_ops):
+            code = n[67 + o]
+            op, a, b, rd = code & 0xFF, (code >> 8) & 0xFF, (code >> 16) & 0xFF, (code >> 24) & 0xFF
+            x, y = regs[a], regs[b]
+            v = {1: lambda: x + y, 2: lambda: x - y, 3: lambda: x * y, 4: lambda: x / y,
+                 5: lambda: (x == y).astype(np.float32), 6: lambda: -x, 7: lambda: np.exp(x),
+                 8: lambda: np.log(x), 9: lambda: np.sqrt(x), 10: lambda: np.maximum(x, 0),
+                 11: lambda: (x > 0).astype(np.float32)}[op]()
+            regs.append(_round(v, rd))
+    store(mem, p[0], out_dt, np.arange(count), regs[-1])
+    return 0
+
+
+def s_reduce(mem, p, n, f):
+    n_out, red_len, kind, in_dt, out_dt, nk = n[0:6]
+    kept = strided_index(n[6:6 + nk], n[14:14 + nk])
+    nr = n[22]
+    red = strided_index(n[23:23 + nr], n[31:31 + nr])
+    values = load(mem, p[0], in_dt, kept[:, None] + red[None, :])
+    result = values.sum(axis=1) if kind == 0 else values.max(axis=1)
+    store(mem, p[1], out_dt, np.arange(n_out), _round(result, out_dt))
+    return 0
+
+
+def s_gather(mem, p, n, f):
+    n_ids, rows, row_bytes, id_dt = n[0:4]
+    ids = mem.view(p[1], id_dt, n_ids).astype(np.int64)
+    ids = np.where(ids < 0, ids + rows, ids)
+    bad = (ids < 0) | (ids >= rows)
+    table = mem.flat(p[0], 0).view(np.uint8)[: rows * row_bytes].reshape(rows, row_bytes)
+    out = mem.flat(p[2], 0).view(np.uint8)[: n_ids * row_bytes].reshape(n_ids, row_bytes)
+    out[:] = np.where(bad[:, None], 0, table[np.clip(ids, 0, rows - 1)])
+    return 1 if bad.any() else 0
+
+
+def s_matmul(mem, p, n, f):
+    batch, M, N, K, adt, bdt, cdt, sam, sak, sbk, sbn, nb = n[0:12]
+    bsizes = n[12:12 + nb]
+    bidx_a = strided_index(bsizes, n[16:16 + nb])
+    bidx_b = strided_index(bsizes, n[20:20 + nb])
+    a_idx = bidx_a[:, None, None] + (np.arange(M)[:, None] * sam + np.arange(K)[None, :] * sak)[None]
+    b_idx = bidx_b[:, None, None] + (np.arange(K)[:, None] * sbk + np.arange(N)[None, :] * sbn)[None]
+    A = load(mem, p[0], adt, a_idx)
+    B = load(mem, p[1], bdt, b_idx)
+    C = np.matmul(A.astype(np.float64), B.astype(np.float64)).astype(np.float32)
+    store(mem, p[2], cdt, np.arange(batch * M * N), _round(C.reshape(-1), cdt))
+    return 0
+
+
+def s_softmax(mem, p, n, f):
+    rows, length, dt, is_, os_, nk = n[0:6]
+    kin = strided_index(n[6:6 + nk], n[14:14 + nk])
+    kout = strided_index(n[6:6 + nk], n[22:22 + nk])
+    x = load(mem, p[0], dt, kin[:, None] + np.arange(length)[None, :] * is_)
+    with np.errstate(all="ignore"):
+        e = _round(np.exp(_round(x - x.max(axis=1, keepdims=True), dt)), dt)
+        s = _round(e.sum(axis=1, keepdims=True), dt)
+        y = _round(e / s, dt)
+    store(mem, p[1], dt, (kout[:, None] + np.arange(length)[None, :] * os_).reshape(-1), y.reshape(-1))
+    return 0
+
+
+def _rms(x, w, eps, dt):
+    ss = _round(_round(x * x, dt).sum(axis=-1, keepdims=True), dt)
+    mean = _round(ss / _round(np.float32(x.shape[-1]), dt), dt)
+    r = _round(np.sqrt(_round(mean + _round(np.float32(eps), dt), dt)), dt)
+    return _round(_round(x / r, dt) * w, dt)
+
+
+def s_rmsnorm(mem, p, n, f):
+    rows, D, rs, dt, wdt = n[0:5]
+    x = load(mem, p[0], dt, np.arange(rows)[:, None] * rs + np.arange(D)[None, :])
+    w = load(mem, p[1], wdt, np.arange(D))
+    store(mem, p[2], dt, np.arange(rows * D), _rms(x, w, f[0], dt).reshape(-1))
+    return 0
+
+
+def s_rope(mem, p, n, f):
+    B, H, T, hd = n[0:4]
+    xs = n[4:8]
+    dt, mode, offset, length = n[8:12]
+    half = hd // 2
+    error = 0
+    out = np.zeros((B, H, T, hd), np.float32)
+    for b in range(B):
+        for t in range(T):
+            pos = offset + t
+            if mode == 1:
+                pos += int(mem.view(p[1], 3, 1)[0])
+            if mode == 2:
+                pos += int(mem.view(p[1], 3, B)[b])
+            if not 0 <= pos < length:
+                error |= 2
+                continue
+            c = load(mem, p[2], dt, pos * hd + np.arange(half))
+            s = load(mem, p[2], dt, pos * hd + half + np.arange(half))
+            for h in range(H):
+                base = b * xs[0] + h * xs[1] + t * xs[2]
+                x1 = load(mem, p[0], dt, base + np.arange(half) * xs[3])
+                x2 = load(mem, p[0], dt, base + (np.arange(half) + half) * xs[3])
+                out[b, h, t, :half] = x1 * c + x2 * -s
+                out[b, h, t, half:] = x1 * s + x2 * c
+    store(mem, p[3], dt, np.arange(out.size), out.reshape(-1))
+    return error
+
+
+def s_sdpa(mem, p, n, f):
+    B, H, T, C, hd, KV, dt = n[0:7]
+    qs, ks, vs, ms = n[7:11], n[11:15], n[15:19], n[19:23]
+    mdt = n[23]
+    div = _round(np.float32(f[0]), dt)
+    out = np.zeros((B, H, T, hd), np.float32)
+    with np.errstate(all="ignore"):
+        for b in range(B):
+            for h in range(H):
+                g = h // (H // KV)
+                K = load(mem, p[1], dt, b * ks[0] + g * ks[1] + np.arange(C)[:, None] * ks[2] + np.arange(hd)[None, :] * ks[3])
+                V = load(mem, p[2], dt, b * vs[0] + g * vs[1] + np.arange(C)[:, None] * vs[2] + np.arange(hd)[None, :] * vs[3])
+                for t in range(T):
+                    q = load(mem, p[0], dt, b * qs[0] + h * qs[1] + t * qs[2] + np.arange(hd) * qs[3])
+                    s = _round(_round((K.astype(np.float64) @ q).astype(np.float32), dt) / div, dt)
+                    if p[3][0] >= 0:
+                        m = load(mem, p[3], mdt, b * ms[0] + h * ms[1] + t * ms[2] + np.arange(C) * ms[3])
+                        s = _round(s + m, dt)
+                    e = _round(np.exp(_round(s - s.max(), dt)), dt)
+                    S = _round(e.sum(), dt)
+                    out[b, h, t] = (_round(e / S, dt).astype(np.float64) @ V).astype(np.float32)
+    store(mem, p[4], dt, np.arange(out.size), out.reshape(-1))
+    return 0
+
+
+def _blend(c, x, w, dt):
+    return _round(_round(c * _round(1 - w, dt), dt) + _round(x * w, dt), dt)
+
+
+def s_kv_write(mem, p, n, f):
+    B, KV, C, hd, dt = n[0:5]
+    xs = n[5:9]
+    wsb, wsr, in_place = n[9:12]
+    cs = n[12:16]
+    wdt = n[16]
+    for b in range(B):
+        w = load(mem, p[2], wdt, b * wsb + np.arange(C) * wsr)
+        for g in range(KV):
+            cidx = b * cs[0] + g * cs[1] + np.arange(C)[:, None] * cs[2] + np.arange(hd)[None, :] * cs[3]
+            xidx = b * xs[0] + g * xs[1] + np.arange(C)[:, None] * xs[2] + np.arange(hd)[None, :] * xs[3]
+            c = load(mem, p[0], dt, cidx)
+            x = load(mem, p[1], dt, xidx)
+            new = _blend(c, x, w[:, None], dt)
+            if in_place:
+                rows = w != 0
+                store(mem, p[3], dt, cidx[rows].reshape(-1), new[rows].reshape(-1))
+            else:
+                base = ((b * KV + g) * C) * hd
+                store(mem, p[3], dt, base + np.arange(C * hd), new.reshape(-1))
+    return 0
+
+
+def s_kv_place(mem, p, n, f):
+    B, KV, C, hd, dt, T = n[0:6]
+    xs = n[6:10]
+    pls = n[10:12]
+    wsb, wsr, in_place = n[12:15]
+    cs = n[15:19]
+    pdt, wdt = n[19:21]
+    pl = load(mem, p[2], pdt, np.arange(T)[:, None] * pls[0] + np.arange(C)[None, :] * pls[1])
+    for b in range(B):
+        w = load(mem, p[3], wdt, b * wsb + np.arange(C) * wsr)
+        touched = (w != 0) | (pl != 0).any(axis=0)
+        for g in range(KV):
+            x = load(mem, p[1], dt, b * xs[0] + g * xs[1] + np.arange(T)[:, None] * xs[2] + np.arange(hd)[None, :] * xs[3])
+            placed = _round((pl.T.astype(np.float64) @ x).astype(np.float32), dt)
+            cidx = b * cs[0] + g * cs[1] + np.arange(C)[:, None] * cs[2] + np.arange(hd)[None, :] * cs[3]
+            c = load(mem, p[0], dt, cidx)
+            new = _round(_round(c * _round(1 - w[:, None], dt), dt) + placed, dt)
+            if in_place:
+                store(mem, p[4], dt, cidx[touched].reshape(-1), new[touched].reshape(-1))
+            else:
+                store(mem, p[4], dt, ((b * KV + g) * C) * hd + np.arange(C * hd), new.reshape(-1))
+    return 0
+
+
+def s_gemv(mem, p, n, f):
+    M, K, xs, dt, nseg, pro, silu = n[0:7]
+    Ns = n[7:11]
+    ostr = n[11:15]
+    rstr = n[15:19]
+    wdt = n[19]
+    x = load(mem, p[0], dt, np.arange(M)[:, None] * xs + np.arange(K)[None, :])
+    if pro:
+        x = _rms(x, load(mem, p[1], wdt, np.arange(K)), f[0], dt)
+    with np.errstate(all="ignore"):
+        if silu:
+            N = Ns[0]
+            g = _round((x.astype(np.float64) @ load(mem, p[2], dt, np.arange(N)[:, None] * K + np.arange(K)[None, :]).T.astype(np.float64)).astype(np.float32), dt)
+            u = _round((x.astype(np.float64) @ load(mem, p[3], dt, np.arange(N)[:, None] * K + np.arange(K)[None, :]).T.astype(np.float64)).astype(np.float32), dt)
+            act = _round(_round(g / _round(_round(np.exp(-g), dt) + 1, dt), dt) * u, dt)
+            store(mem, p[6], dt, (np.arange(M)[:, None] * ostr[0] + np.arange(N)[None, :]).reshape(-1), act.reshape(-1))
+            return 0
+        for s in range(nseg):
+            N = Ns[s]
+            W = load(mem, p[2 + s], dt, np.arange(N)[:, None] * K + np.arange(K)[None, :])
+            y = _round((x.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32), dt)
+            if p[10 + s][0] >= 0:
+                res = load(mem, p[10 + s], dt, np.arange(M)[:, None] * rstr[s] + np.arange(N)[None, :])
+                y = _round(res + y, dt)
+            store(mem, p[6 + s], dt, (np.arange(M)[:, None] * ostr[s] + np.arange(N)[None, :]).reshape(-1), y.reshape(-1))
+    return 0
+
+
+STEP = {
+    P.K_FILL: s_fill, P.K_COPY: s_copy, P.K_ELEMENTWISE: s_elementwise, P.K_REDUCE: s_reduce,
+    P.K_GATHER: s_gather, P.K_MATMUL: s_matmul, P.K_SOFTMAX: s_softmax, P.K_RMSNORM: s_rmsnorm,
+    P.K_ROPE: s_rope, P.K_SDPA: s_sdpa, P.K_KV_WRITE: s_kv_write, P.K_KV_PLACE: s_kv_place,
+    P.K_GEMV: s_gemv,
+}

@@ -1,0 +1,193 @@
+"""The hip plugin against the oracle on the six IR ops and the fused kernels
+(plugin conformance, after the reference's tests/test_cuda.py and
+tests/test_mlx.py, aimed at compiler="hip")."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from chomikgrad import Tensor, compile_graph, realize
+from chomikgrad.dtypes import BFLOAT16, bf16_to_float32, to_bf16
+from chomikgrad.hip_backend import HIPArray
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(name):
+    print(f"[gpu case] {name}", flush=True)
+
+
+def as_float(values):
+    values = np.asarray(values)
+    return bf16_to_float32(values) if values.dtype == BFLOAT16 else values.astype(np.float32)
+
+
+def both(*tensors):
+    return realize(*tensors, compiler="hip"), realize(*tensors, compiler="cpu")
+
+
+def test_six_ir_operations_and_gather_match_cpu(hip):
+    announce("six ops + gather")
+    left = Tensor([[1.0, -2.0, 0.5], [3.0, 4.0, -1.0]], dtype=np.float32)
+    right = Tensor([[2.0, 1.0], [-1.0, 0.5], [3.0, -2.0]], dtype=np.float32)
+    result = ((left @ right).relu() + 0.25).permute(1, 0).reshape(1, 4).sum(axis=1)
+    program = compile_graph(result, compiler="hip")
+    np.testing.assert_allclose(program()[0], result.numpy(compiler="cpu"), rtol=1e-5, atol=1e-6)
+    assert "fused_elementwise" in program.source and "matmul" in program.source
+    table = Tensor([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], dtype=np.float32)
+    gathered = table.gather(Tensor(np.array([[2, 0, -3]], dtype=np.int32), copy=False))
+    gather_program = compile_graph(gathered, compiler="hip")
+    assert "gather" in gather_program.source
+    np.testing.assert_allclose(gather_program()[0], [[[5.0, 6.0], [1.0, 2.0], [1.0, 2.0]]])
+
+
+def test_gather_index_outside_table_raises_index_error(hip):
+    announce("gather out of range -> IndexError")
+    table = Tensor(np.arange(6, dtype=np.float32).reshape(3, 2))
+    with pytest.raises(IndexError):
+        table.gather(Tensor(np.array([5], dtype=np.int64))).numpy(compiler="hip")
+    # the error is cleared: the next program runs normally
+    np.testing.assert_allclose(table.gather(Tensor(np.array([1], np.int64))).numpy(compiler="hip"), [[2.0, 3.0]])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, BFLOAT16])
+def test_batched_matmul_matches_cpu(hip, dtype):
+    announce(f"batched matmul {np.dtype(dtype)}")
+    rng = np.random.default_rng(19)
+    left = Tensor(rng.normal(size=(2, 4, 3, 5)).astype(np.float32), dtype=dtype)
+    right = Tensor(rng.normal(size=(2, 4, 5, 6)).astype(np.float32), dtype=dtype)
+    weight = Tensor(rng.normal(size=(5, 7)).astype(np.float32), dtype=dtype)
+    outputs = [left @ right, left @ weight, Tensor(rng.normal(size=(1, 3, 5)).astype(np.float32), dtype=dtype) @ weight]
+    got, expected = both(*outputs)
+    tolerance = 1e-5 if dtype == np.float32 else 1e-2
+    for g, e in zip(got, expected):
+        np.testing.assert_allclose(as_float(g), as_float(e), rtol=tolerance, atol=tolerance)
+
+
+def test_dynamic_input_and_deferred_synchronization(hip):
+    announce("dynamic input rebinding")
+    source = Tensor([1.0, 2.0], dtype=np.float32)
+    program = compile_graph(source * 2.0, compiler="hip", dynamic_inputs=(source,))
+    replacement = hip.device.array(np.array([3.0, 4.0], dtype=np.float32))
+    native = program.run({source._node: replacement}, synchronize=False)[0]
+    program.device.synchronize()
+    assert isinstance(native, HIPArray)
+    np.testing.assert_allclose(program.device.to_numpy(native), [6.0, 8.0])
+    np.testing.assert_allclose(program()[0], [2.0, 4.0])
+    assert program.inputs == (source._node,)
+    assert program.device.argmax(native) == 1
+    np.testing.assert_array_equal(program.device.argmax_last_axis(native), 1)
+
+
+def test_argmax_follows_numpy_first_occurrence_and_nan(hip):
+    announce("argmax ties and NaN")
+    device = hip.device
+    values = np.array([[1.0, 5.0, 5.0, 2.0], [np.nan, 1.0, np.nan, 9.0], [-np.inf] * 4], dtype=np.float32)
+    native = device.array(values)
+    np.testing.assert_array_equal(device.argmax_last_axis(native), values.argmax(axis=-1))
+    big = np.random.default_rng(0).normal(size=32000).astype(np.float16)
+    big[[7, 31000]] = np.float16(60000.0)
+    assert device.argmax(device.array(big)) == 7
+
+
+def test_copy_false_observes_host_mutation(hip):
+    announce("copy=False re-uploads")
+    source = np.array([1.0, 2.0], dtype=np.float32)
+    tensor = Tensor(source, copy=False)
+    np.testing.assert_allclose(tensor.numpy(compiler="hip"), [1.0, 2.0])
+    source[0] = 9.0
+    np.testing.assert_allclose((tensor * 1.0).numpy(compiler="hip"), [9.0, 2.0])
+
+
+def test_softmax_reductions_and_elementwise_chains(hip):
+    announce("softmax/reduce/elementwise")
+    rng = np.random.default_rng(29)
+    for dtype in (np.float32, np.float16):
+        source = Tensor(rng.normal(size=(3, 5, 64)).astype(dtype))
+        outputs = [source.softmax(axis=-1), source.softmax(axis=1), source.max(axis=(0, 2), keepdims=True),
+                   source.sum(), (source.exp() * 2.0 - source.relu().sqrt()).mean(axis=-1),
+                   source.log_softmax(axis=-1), source.layer_norm(Tensor(np.ones(64, dtype)), Tensor(np.zeros(64, dtype)))]
+        got, expected = both(*outputs)
+        tolerance = 2e-5 if dtype == np.float32 else 2e-3
+        for g, e in zip(got, expected):
+            np.testing.assert_allclose(as_float(g), as_float(e), rtol=tolerance, atol=tolerance)
+
+
+def test_structural_program_cache_and_leaf_aliasing(hip):
+    announce("program cache")
+    first = Tensor([1.0, 2.0], dtype=np.float32).relu().softmax()
+    first.numpy(compiler="hip")
+    size = hip.cache_size
+    Tensor([3.0, 4.0], dtype=np.float32).relu().softmax().numpy(compiler="hip")
+    assert hip.cache_size == size
+    left, right = Tensor([1.0, 2.0], dtype=np.float32), Tensor([10.0, 20.0], dtype=np.float32)
+    np.testing.assert_allclose((left + left).numpy(compiler="hip"), [2.0, 4.0])
+    np.testing.assert_allclose((left + right).numpy(compiler="hip"), [11.0, 22.0])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, BFLOAT16])
+@pytest.mark.parametrize("rows", [1, 3, 8])
+def test_gemv_linear_variants(hip, dtype, rows):
+    announce(f"gemv {np.dtype(dtype)} rows={rows}")
+    rng = np.random.default_rng(rows)
+    K, N = 512, 384
+    x = Tensor(rng.normal(size=(1, rows, K)).astype(np.float32), dtype=dtype)
+    h = Tensor(rng.normal(size=(1, rows, N)).astype(np.float32), dtype=dtype)
+    norm = Tensor(np.ones(K, np.float32), dtype=dtype)
+    w1 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
+    w2 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
+    w3 = Tensor((rng.normal(size=(K, N)) * 0.05).astype(np.float32), dtype=dtype)
+    variance = (x * x).mean(axis=-1, keepdims=True)
+    normed = x / (variance + 1e-5).sqrt() * norm
+    normed._node.lowering = ("rms_norm", (x._node, norm._node), 1e-5)
+    gate = normed @ w1.T
+    act = gate / (1 + (-gate).exp()) * (normed @ w2.T)
+    outputs = [x @ w1.T, h + (x @ w1.T), act, act @ w3.T]
+    program = compile_graph(*outputs, compiler="hip")
+    assert "gemv" in program.source
+    got = program()
+    expected = realize(*outputs, compiler="cpu")
+    tolerance = 1e-4 if dtype == np.float32 else 3e-2
+    for g, e in zip(got, expected):
+        np.testing.assert_allclose(as_float(g), as_float(e), rtol=tolerance, atol=tolerance)
+
+
+def test_empty_tensors(hip):
+    announce("empty tensors")
+    empty = Tensor(np.empty((0, 4), dtype=np.float32))
+    assert empty.softmax(axis=-1).numpy(compiler="hip").shape == (0, 4)
+    assert (empty * 2.0).numpy(compiler="hip").shape == (0, 4)
+    np.testing.assert_allclose(empty.sum(axis=0).numpy(compiler="hip"), np.zeros(4))
+
+
+def test_float64_is_rejected(hip):
+    announce("float64 rejected")
+    with pytest.raises(TypeError):
+        (Tensor([1.0, 2.0]) * 2.0).numpy(compiler="hip")
+
+
+def test_safetensors_loading(hip, tmp_path):
+    announce("safetensors")
+    import json
+    import struct
+
+    weights = {"a": np.arange(6, dtype=np.float32).reshape(2, 3), "b": np.ones(4, np.float16)}
+    header, blobs, offset = {}, [], 0
+    for name, value in weights.items():
+        raw = value.tobytes()
+        header[name] = {"dtype": {"float32": "F32", "float16": "F16"}[value.dtype.name],
+                        "shape": list(value.shape), "data_offsets": [offset, offset + len(raw)]}
+        blobs.append(raw)
+        offset += len(raw)
+    blob = json.dumps(header).encode()
+    path = tmp_path / "w.safetensors"
+    path.write_bytes(struct.pack("<Q", len(blob)) + blob + b"".join(blobs))
+    from chomikgrad.llama import load_safetensors
+
+    loaded = load_safetensors(path, hip.device, dtype=np.float16)
+    assert loaded["a"].dtype == np.float16 and loaded["a"].shape == (2, 3)
+    np.testing.assert_array_equal(loaded["a"].numpy(compiler="hip"), weights["a"].astype(np.float16))
+    bf = load_safetensors(path, hip.device, dtype=BFLOAT16)
+    np.testing.assert_array_equal(bf["b"].numpy(compiler="hip").view(np.uint16),
+                                  to_bf16(np.ones(4, np.float32)).view(np.uint16))

@@ -1,0 +1,232 @@
+"""The hip plugin's planner on CPU: lowering choice, fusion passes, memory
+plan and tape encoding, executed by the host tape model (tests/tape_model.py)
+and compared with the oracle.  No GPU is involved; the GPU tests repeat the
+same cases through libchomik_hip.so."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from chomikgrad import Tensor, realize, synthetic
+from chomikgrad._planner import K_GEMV, K_KV_PLACE, K_KV_WRITE, K_SDPA, plan_graph
+from chomikgrad.dtypes import BFLOAT16, bf16_to_float32, to_bf16
+from chomikgrad.llama import (
+    LlamaBatchedDecoderStep,
+    LlamaConfig,
+    LlamaDecoderBlock,
+    LlamaDecoderStep,
+    LlamaForCausalLM,
+    _rope_rotations,
+    block_masks,
+    decode_masks,
+    position_selector,
+)
+from conftest import tiny_weights
+from tape_model import CpuPlanCompiler, run
+
+COMPILER = CpuPlanCompiler()
+
+
+def model_run(outputs, dynamic=(), donate=(), bindings=None):
+    nodes = [t._node for t in outputs]
+    planned = plan_graph(COMPILER, nodes, [t._node for t in dynamic], [t._node for t in donate])
+    values = {}
+    for leaf in planned.input_slots:
+        values[leaf] = (bindings or {}).get(leaf, leaf.numpy_value() if leaf.value is not None else None)
+    return planned, run(planned, values)
+
+
+def as_float(values):
+    values = np.asarray(values)
+    return bf16_to_float32(values) if values.dtype == BFLOAT16 else values.astype(np.float32)
+
+
+def test_six_ops_and_gather_match_oracle():
+    left = Tensor([[1.0, -2.0, 0.5], [3.0, 4.0, -1.0]], dtype=np.float32)
+    right = Tensor([[2.0, 1.0], [-1.0, 0.5], [3.0, -2.0]], dtype=np.float32)
+    result = ((left @ right).relu() + 0.25).permute(1, 0).reshape(1, 4).sum(axis=1)
+    planned, got = model_run([result])
+    np.testing.assert_allclose(got[0], result.numpy(compiler="cpu"), rtol=1e-5, atol=1e-6)
+    assert "fused_elementwise" in planned.source and "matmul" in planned.source
+    table = Tensor([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], dtype=np.float32)
+    ids = Tensor(np.array([[2, 0, -1]], dtype=np.int32), copy=False)
+    _, got = model_run([table.gather(ids)])
+    np.testing.assert_allclose(got[0], [[[5.0, 6.0], [1.0, 2.0], [5.0, 6.0]]])
+
+
+def test_gather_out_of_range_raises():
+    table = Tensor([[1.0, 2.0]], dtype=np.float32)
+    with pytest.raises(IndexError):
+        model_run([table.gather(Tensor(np.array([1], dtype=np.int32)))])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16, BFLOAT16])
+def test_batched_and_broadcast_matmul(dtype):
+    rng = np.random.default_rng(19)
+    left = Tensor(rng.normal(size=(2, 4, 3, 5)).astype(np.float32), dtype=dtype)
+    right = Tensor(rng.normal(size=(2, 4, 5, 6)).astype(np.float32), dtype=dtype)
+    weight = Tensor(rng.normal(size=(5, 7)).astype(np.float32), dtype=dtype)
+    outputs = [left @ right, left @ weight, (left.transpose(-2, -1).transpose(-2, -1)) @ right]
+    _, got = model_run(outputs)
+    for out, value in zip(outputs, got):
+        np.testing.assert_allclose(as_float(value), as_float(out.numpy(compiler="cpu")), rtol=1e-2, atol=1e-2)
+
+
+def test_softmax_reductions_and_elementwise_chains():
+    rng = np.random.default_rng(29)
+    source = Tensor(rng.normal(size=(2, 3, 4)).astype(np.float16))
+    outputs = [source.softmax(axis=1), source.softmax(axis=-1), source.max(axis=(0, 2), keepdims=True),
+               (source.exp() * 2.0 - source.sqrt()).mean(axis=-1), source.log_softmax(axis=-1)]
+    _, got = model_run(outputs)
+    for out, value in zip(outputs, got):
+        expected = out.numpy(compiler="cpu")
+        np.testing.assert_allclose(value.astype(np.float32), expected.astype(np.float32),
+                                   rtol=2e-3, atol=2e-3, equal_nan=True)
+
+
+def test_linear_uses_gemv_with_fusions():
+    config = synthetic.TINY.config
+    weights = tiny_weights(config, 1)
+    C = 20
+    position = 7
+    dec = LlamaDecoderStep(config, weights, cache_length=C, dtype=np.float32)
+    attention, write = decode_masks(position, C, np.float32)
+    leaves = [Tensor(np.array([[5]], np.int32), copy=False),
+              Tensor(_rope_rotations(1, 64, config.rope_theta, np.float32, offset=position), copy=False),
+              Tensor(attention, copy=False), Tensor(write, copy=False),
+              Tensor(np.asarray(position, np.int32), copy=False)]
+    rng = np.random.default_rng(2)
+    caches = [Tensor(rng.normal(size=(1, 2, C, 64)).astype(np.float32), copy=False) for _ in range(4)]
+    outputs = dec(*leaves[:4], list(zip(caches[::2], caches[1::2])), position=leaves[4])
+    expected = realize(*outputs, compiler="cpu")
+    planned, got = model_run(outputs, leaves + caches, donate=caches)
+    kinds = [s.kind for s in planned.steps]
+    assert kinds.count(K_GEMV) == 4 * config.num_hidden_layers + 1
+    assert kinds.count(K_KV_WRITE) == 2 * config.num_hidden_layers
+    assert kinds.count(K_SDPA) == config.num_hidden_layers
+    assert "gemv[rms_norm]" in planned.source and "gemv[rms_norm+silu_mul]" in planned.source
+    assert "gemv[residual]" in planned.source
+    for value, reference in zip(got, expected):
+        np.testing.assert_allclose(value, reference, rtol=1e-4, atol=1e-5)
+    # Donated caches are updated in place: the outputs are the input leaves.
+    assert [spec[0] for spec in planned.output_specs[1:]] == ["input"] * 4
+
+
+def _fp16_layer():
+    config = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1408, num_hidden_layers=1,
+                         num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=256)
+    host = synthetic.host_weights(config, np.float16, seed=7)
+    return config, synthetic.weights_as_tensors(host)
+
+
+def test_fp16_decode_step_is_bit_exact_with_oracle_roundings():
+    config, weights = _fp16_layer()
+    C, position = 24, 11
+    rng = np.random.default_rng(4)
+    caches = [Tensor((rng.normal(size=(1, 2, C, 64)) * 0.5).astype(np.float16), copy=False) for _ in range(2)]
+    attention, write = decode_masks(position, C, np.float16)
+    leaves = [Tensor(np.array([[17]], np.int32), copy=False),
+              Tensor(_rope_rotations(1, 64, config.rope_theta, np.float16, offset=position), copy=False),
+              Tensor(attention, copy=False), Tensor(write, copy=False),
+              Tensor(np.asarray(position, np.int32), copy=False)]
+    dec = LlamaDecoderStep(config, weights, cache_length=C, dtype=np.float16)
+    outputs = dec(*leaves[:4], [(caches[0], caches[1])], position=leaves[4])
+    expected = realize(*outputs, compiler="cpu")
+    _, got = model_run(outputs, leaves + caches)
+    # The fused kernels round where the portable graph rounds; only the
+    # order of float32 sums differs.  An occasional one-ulp flip in the hidden
+    # state moves many logits by an ulp, but most stay bit-identical (without
+    # the matching roundings almost none would).
+    np.testing.assert_allclose(got[0].astype(np.float32), expected[0].astype(np.float32), atol=2e-3, rtol=2e-3)
+    assert np.mean(got[0] == expected[0]) > 0.5
+    for value, reference in zip(got[1:], expected[1:]):
+        np.testing.assert_allclose(value.astype(np.float32), reference.astype(np.float32), atol=2e-3, rtol=1e-2)
+        assert np.mean(value == reference) > 0.99
+
+
+def test_prefill_with_cache_placement():
+    config = synthetic.TINY.config
+    weights = tiny_weights(config, 9)
+    model = LlamaForCausalLM(config, weights, sequence_length=6, cache_length=10, dtype=np.float32)
+    tokens = Tensor(np.array([[1, 5, 9, 2, 4, 3]], np.int32), copy=False)
+    outputs = model.prefill(tokens, Tensor(position_selector(5, 6, dtype=np.float32)))
+    expected = realize(*outputs, compiler="cpu")
+    _, got = model_run(outputs, [tokens])
+    for value, reference in zip(got, expected):
+        np.testing.assert_allclose(value, reference, rtol=1e-4, atol=1e-5)
+
+
+def test_block_verify_uses_kv_place():
+    config = synthetic.TINY.config
+    weights = tiny_weights(config, 10)
+    C, position, n = 12, 6, 3
+    rng = np.random.default_rng(1)
+    caches = [Tensor(rng.normal(size=(1, 2, C, 64)).astype(np.float32), copy=False) for _ in range(4)]
+    placement, write, attention = block_masks(position, n, C, np.float32)
+    block = LlamaDecoderBlock(config, weights, block_length=n, cache_length=C, dtype=np.float32)
+    leaves = [Tensor(np.array([[3, 8, 1]], np.int32), copy=False),
+              Tensor(_rope_rotations(n, 64, config.rope_theta, np.float32, offset=position), copy=False),
+              Tensor(attention, copy=False), Tensor(placement, copy=False), Tensor(write, copy=False),
+              Tensor(np.asarray(position, np.int32), copy=False)]
+    outputs = block(*leaves[:5], list(zip(caches[::2], caches[1::2])), position=leaves[5])
+    expected = realize(*outputs, compiler="cpu")
+    planned, got = model_run(outputs, leaves + caches, donate=caches)
+    assert any(s.kind == K_KV_PLACE for s in planned.steps)
+    for value, reference in zip(got, expected):
+        np.testing.assert_allclose(value, reference, rtol=1e-4, atol=1e-5)
+
+
+def test_batched_bf16_decode():
+    config = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=1,
+                         num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64,
+                         rope_theta=500_000.0)
+    host = synthetic.host_weights(config, BFLOAT16, seed=3, tie_embeddings=True)
+    weights = synthetic.weights_as_tensors(host)
+    B, C = 3, 16
+    positions = np.array([4, 9, 2], np.int32)
+    rng = np.random.default_rng(6)
+    caches = [Tensor(to_bf16(rng.normal(size=(B, 2, C, 64)) * 0.3), copy=False) for _ in range(2)]
+    attention = np.concatenate([decode_masks(int(p), C, np.float32)[0] for p in positions]).reshape(B, 1, 1, C)
+    write = np.concatenate([decode_masks(int(p), C, np.float32)[1] for p in positions]).reshape(B, 1, C, 1)
+    rotation = np.concatenate([_rope_rotations(1, 64, config.rope_theta, np.float32, offset=int(p))
+                               for p in positions]).reshape(B, 1, 1, 64, 64)
+    leaves = [Tensor(np.array([[1], [7], [200]], np.int32), copy=False),
+              Tensor(to_bf16(rotation), copy=False), Tensor(to_bf16(attention), copy=False),
+              Tensor(to_bf16(write), copy=False), Tensor(positions, copy=False)]
+    dec = LlamaBatchedDecoderStep(config, weights, batch=B, cache_length=C, dtype=BFLOAT16)
+    outputs = dec(*leaves[:4], [(caches[0], caches[1])], position=leaves[4])
+    expected = realize(*outputs, compiler="cpu")
+    planned, got = model_run(outputs, leaves + caches)
+    assert "gemv" in planned.source
+    np.testing.assert_allclose(as_float(got[0]), as_float(expected[0]), atol=3e-2, rtol=3e-2)
+    for value, reference in zip(got[1:], expected[1:]):
+        np.testing.assert_allclose(as_float(value), as_float(reference), atol=2e-2, rtol=2e-2)
+
+
+def test_dynamic_inputs_are_validated():
+    from chomikgrad.hip_backend import HIPCompiler
+
+    source = Tensor([1.0, 2.0], dtype=np.float32)
+    other = Tensor([3.0], dtype=np.float32)
+    with pytest.raises(ValueError):
+        HIPCompiler.compile(COMPILER, [(source * 2.0)._node], [(source * 3.0)._node])
+    with pytest.raises(ValueError):
+        HIPCompiler.compile(COMPILER, [(source * 2.0)._node], [other._node])
+    with pytest.raises(ValueError):
+        HIPCompiler.compile(COMPILER, [], [])
+
+
+def test_float64_is_rejected():
+    with pytest.raises(TypeError):
+        plan_graph(COMPILER, [(Tensor([1.0, 2.0]) * 2.0)._node], [])
+
+
+def test_memory_plan_reuses_the_arena():
+    x = Tensor(np.ones((64, 64), np.float32))
+    y = x
+    for _ in range(8):
+        y = (y @ x).relu()
+    planned = plan_graph(COMPILER, [y._node], [])
+    per_value = 64 * 64 * 4
+    assert planned.arena_bytes <= 3 * per_value

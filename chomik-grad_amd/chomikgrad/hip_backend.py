@@ -140,8 +140,9 @@ class HIPDeviceAdapter(DeviceAdapter):
         if host.dtype == np.bool_:
             host = host.astype(np.int32)
         dtype_code(host.dtype)
-        host = np.ascontiguousarray(host)
-        result = self.empty(host.shape, host.dtype)
+        shape = host.shape
+        host = np.ascontiguousarray(host)  # (0-d arrays come back 1-d)
+        result = self.empty(shape, host.dtype)
         if result.ptr:
             self.lib.call("chip_memcpy_h2d", ctypes.c_void_p(result.ptr),
                           host.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(host.nbytes), 1)

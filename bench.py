@@ -128,7 +128,7 @@ def cpu_baseline(config, weights, dtype, context: int, first_position: int, step
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=127)
+    parser.add_argument("--steps", type=int, default=115)
     parser.add_argument("--warmup", type=int, default=8)
     parser.add_argument("--timing-runs", type=int, default=4, help="decode steps timed per kernel")
     parser.add_argument("--cpu-steps", type=int, default=3, help="oracle decode steps for the CPU baseline")

@@ -26,6 +26,7 @@ Stages
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Set, Tuple
 
@@ -37,12 +38,13 @@ from .lazy import GraphPlan, LazyNode, Op
 # Step kinds (enum chip_kind in include/chomik_hip.h).
 K_FILL, K_COPY, K_ELEMENTWISE, K_REDUCE, K_GATHER, K_MATMUL, K_SOFTMAX = 1, 2, 3, 4, 5, 6, 7
 K_RMSNORM, K_ROPE, K_SDPA, K_KV_WRITE, K_KV_PLACE, K_GEMV, K_GEMM = 8, 9, 10, 11, 12, 13, 14
+K_DECODE_ATTN = 17
 
 KIND_NAMES = {
     K_FILL: "fill", K_COPY: "copy", K_ELEMENTWISE: "fused_elementwise",
     K_REDUCE: "reduce", K_GATHER: "gather", K_MATMUL: "matmul", K_SOFTMAX: "softmax",
     K_RMSNORM: "rms_norm", K_ROPE: "rope", K_SDPA: "sdpa", K_KV_WRITE: "kv_write",
-    K_KV_PLACE: "kv_place", K_GEMV: "gemv", K_GEMM: "gemm",
+    K_KV_PLACE: "kv_place", K_GEMV: "gemv", K_GEMM: "gemm", K_DECODE_ATTN: "decode_attention",
 }
 
 OPCODES = {"add": 1, "sub": 2, "mul": 3, "div": 4, "equal": 5, "neg": 6, "exp": 7,
@@ -52,6 +54,9 @@ MAX_EW_INPUTS = 6
 MAX_EW_OPS = 24
 GEMV_MAX_ROWS = 8
 GEMV_STAGE_BYTES = 48 * 1024
+# Waves sharing one GEMV row group (K split): 0 lets the kernel choose from
+# the row count; CHOMIK_HIP_GEMV_SPLIT=1/2/4 forces one (for tuning sweeps).
+GEMV_SPLIT = int(os.environ.get("CHOMIK_HIP_GEMV_SPLIT", "0"))
 SDPA_MAX_KEYS = 32768
 ARENA_ALIGN = 256
 SUPPORTED_TAGS = frozenset({"rms_norm", "rope", "sdpa", "softmax"})
@@ -389,6 +394,14 @@ class Emitter:
         self.constants.append(native)
         storage = self.new_storage("const", host.nbytes, native=native, label=label)
         return PV(host.shape, host.dtype, contiguous_strides(host.shape), storage)
+
+    def zeros(self, nbytes: int, label: str) -> PV:
+        """A zero-filled device buffer owned by the program (kernel scratch
+        such as self-resetting tickets)."""
+        native = self.compiler.device.zeros((max(nbytes // 4, 1),), np.int32)
+        self.constants.append(native)
+        storage = self.new_storage("const", native.nbytes, native=native, label=label)
+        return PV(native.shape, np.int32, (1,), storage)
 
     def add(self, kind: int, ins, outs, **attrs) -> Step:
         step = Step(kind, list(ins), list(outs), dict(attrs))
@@ -817,6 +830,65 @@ def fuse_residual(steps: List[Step], outputs: List[PV]) -> List[Step]:
     return [s for s in steps if id(s) not in removed]
 
 
+def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitter") -> List[Step]:
+    """rope(q), rope(k), kv_write(K), kv_write(V), sdpa -> one decode_attention
+    step (single new token, head size 64)."""
+    counts = _consumers(steps, outputs)
+    producer = _producer(steps)
+    removed = set()
+    tickets: Optional[PV] = None
+    for index, step in enumerate(steps):
+        if step.kind != K_SDPA:
+            continue
+        q, K, V, mask = step.ins
+        if q.shape[2] != 1 or q.shape[3] != 64:
+            continue
+        found = [producer.get(id(pv.storage)) for pv in (q, K, V)]
+        if any(f is None for f in found):
+            continue
+        rq, wk, wv = (f[1] for f in found)
+        if rq.kind != K_ROPE or wk.kind != K_KV_WRITE or wv.kind != K_KV_WRITE:
+            continue
+        if rq.attrs["mode"] not in (1, 2) or not q.whole() or counts.get(id(q.storage)) != 1:
+            continue
+        cache_k, xk, w = wk.ins
+        cache_v, xv, w2 = wv.ins
+        if not (K.same_data(wk.outs[0]) and V.same_data(wv.outs[0])):
+            continue
+        if w.storage is not w2.storage or w.offset != w2.offset or w.strides != w2.strides:
+            continue
+        if wk.attrs["in_place"] != wv.attrs["in_place"]:
+            continue
+        rk_found = producer.get(id(xk.storage))
+        if rk_found is None:
+            continue
+        rk = rk_found[1]
+        if (rk.kind != K_ROPE or not xk.whole() or counts.get(id(xk.storage)) != 1
+                or rk.ins[1] is None or rk.ins[1].storage is not rq.ins[1].storage
+                or rk.ins[2].storage is not rq.ins[2].storage or rk.attrs != rq.attrs):
+            continue
+        if xv.shape[2] != 1 or rk.ins[0].shape[2] != 1:
+            continue
+        B, H, _, _ = q.shape
+        KV, C = cache_k.shape[1], cache_k.shape[2]
+        if cache_k.shape != cache_v.shape or cache_k.strides != cache_v.strides:
+            continue
+        if cache_k.strides[2:] != (64, 1) or cache_v.strides[2:] != (64, 1):
+            continue
+        if C * 4 > 96 * 1024 or w.dtype != q.dtype or mask.dtype != q.dtype:
+            continue
+        if tickets is None or tickets.size < B * KV:
+            tickets = emitter.zeros(4 * max(B * KV, 64), "tickets")
+        fused = Step(K_DECODE_ATTN,
+                     [rq.ins[0], rk.ins[0], xv, rq.ins[1], rq.ins[2], cache_k, cache_v, w, mask, tickets],
+                     [step.outs[0], wk.outs[0], wv.outs[0]],
+                     {"in_place": wk.attrs["in_place"], "table_length": rq.attrs["table_length"],
+                      "mode": rq.attrs["mode"], "divisor": step.attrs["divisor"]})
+        steps[index] = fused
+        removed.update({id(rq), id(rk), id(wk), id(wv)})
+    return [s for s in steps if id(s) not in removed]
+
+
 def merge_sibling_gemvs(steps: List[Step]) -> List[Step]:
     removed = set()
     for i, first in enumerate(steps):
@@ -1015,6 +1087,22 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         ints += [ws[0], ws[2], 1 if a["in_place"] else 0] + list(cache.strides)
         ints += [dtype_code(placement.dtype), dtype_code(w.dtype)]
         return kind, [_ptr(cache), _ptr(x), _ptr(placement), _ptr(w), _ptr(out)], ints, []
+    if kind == K_DECODE_ATTN:
+        q, k, v, position, table, cache_k, cache_v, w, mask, tickets = step.ins
+        out, out_k, out_v = step.outs
+        B, H = q.shape[0], q.shape[1]
+        KV, C = cache_k.shape[1], cache_k.shape[2]
+        ws = broadcast_strides(w, (B, 1, C, 1))
+        ms = broadcast_strides(mask, (B, H, 1, C))
+        ints = [B, H, KV, C, dtype_code(q.dtype),
+                q.strides[0], q.strides[1], q.strides[3],
+                k.strides[0], k.strides[1], k.strides[3],
+                v.strides[0], v.strides[1], v.strides[3],
+                a["mode"], a["table_length"]] + list(cache_k.strides)
+        ints += [ws[0], ws[2], ms[0], ms[1], ms[3], dtype_code(mask.dtype), dtype_code(w.dtype),
+                 1 if a["in_place"] else 0]
+        ptrs = [_ptr(pv) for pv in (q, k, v, position, table, cache_k, cache_v, w, mask, out, out_k, out_v, tickets)]
+        return kind, ptrs, ints, [a["divisor"]]
     if kind == K_GEMV:
         segments = a["segments"]
         prologue = a["prologue"]
@@ -1034,7 +1122,10 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         else:
             ints += _pad(n, 4)
         ints += _pad([s["res"].shape[-1] if s["res"] is not None else 0 for s in segments], 4)
-        ints += [dtype_code(prologue["w"].dtype) if prologue else 0, 1 if stage else 0]
+        vector = 16 // x.itemsize
+        aligned = x.row_stride() % vector == 0 and (_ptr(x)[1] % 16) == 0
+        ints += [dtype_code(prologue["w"].dtype) if prologue else 0, 1 if stage else 0, GEMV_SPLIT,
+                 1 if aligned else 0]
         return kind, ptrs, ints, [prologue["eps"] if prologue else 0.0]
     raise AssertionError(f"no encoder for step kind {kind}")
 
@@ -1098,6 +1189,7 @@ def plan_graph(compiler, outputs: Sequence[LazyNode], dynamic_inputs: Sequence[L
     steps = fuse_silu_gemv(steps, out_pvs)
     steps = fuse_residual(steps, out_pvs)
     steps = merge_sibling_gemvs(steps)
+    steps = fuse_decode_attention(steps, out_pvs, emitter)
 
     # Program outputs: leaves are returned as they are, whole intermediates
     # become caller-visible buffers, anything else is copied into one.

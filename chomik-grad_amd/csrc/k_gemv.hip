@@ -25,47 +25,32 @@ namespace {
 // n[0] M, n[1] K, n[2] x row stride (elements), n[3] dtype, n[4] segments,
 // n[5] prologue (0 none, 1 rmsnorm), n[6] silu (segments 0/1 = gate/up),
 // n[7..10] N per segment, n[11..14] out row stride, n[15..18] residual row
-// stride, n[19] norm-weight dtype, n[20] stage x in LDS; f[0] eps.
+// stride, n[19] norm-weight dtype, n[20] stage x in LDS, n[21] waves that
+// split K for one row group (0 or 1: one wave per row group), n[22] x rows
+// are 16-byte aligned (vector staging); f[0] eps.
 constexpr int kMaxRows = 8;
 
-template <typename T> __device__ __forceinline__ void unpack(const uint4& v, float* out);
-template <> __device__ __forceinline__ void unpack<__half>(const uint4& v, float* out) {
-  const __half2* h = reinterpret_cast<const __half2*>(&v);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float2 f = __half22float2(h[i]);
-    out[2 * i] = f.x;
-    out[2 * i + 1] = f.y;
-  }
-}
-template <> __device__ __forceinline__ void unpack<bf16_t>(const uint4& v, float* out) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    out[2 * i] = __uint_as_float(w[i] << 16);
-    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-  }
-}
-template <> __device__ __forceinline__ void unpack<float>(const uint4& v, float* out) {
-  out[0] = __uint_as_float(v.x);
-  out[1] = __uint_as_float(v.y);
-  out[2] = __uint_as_float(v.z);
-  out[3] = __uint_as_float(v.w);
-}
-
-template <typename T, int MM, int NR, int U, bool PRO, bool SILU, bool STAGE>
+template <typename T, int MM, int NR, int U, bool PRO, bool SILU, bool STAGE, int SPLIT>
 __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
   using E = Elem<T>;
   constexpr int V = 16 / sizeof(T);
+  constexpr int GROUPS = 4 / SPLIT;  // row groups per block
   extern __shared__ uint4 xs[];  // M x K staged input (T), when STAGE
   __shared__ float red[4];
   __shared__ float rnorm[MM];
+  __shared__ float partial[SPLIT > 1 ? 4 : 1][MM][NR];
 
   const int M = static_cast<int>(a.n[0]);
   const int64_t K = a.n[1], KV = K / V;
   const int dt = E::code;
   const int lane = threadIdx.x & 63;
-  const int64_t wave = blockIdx.x * int64_t(4) + (threadIdx.x >> 6);
+  const int wave_in_block = threadIdx.x >> 6;
+  const int slice = wave_in_block % SPLIT;
+  // the row group this wave works on; SPLIT waves share it, one K slice each
+  const int64_t wave = blockIdx.x * int64_t(GROUPS) + wave_in_block / SPLIT;
+  const int64_t slice_len = (KV + SPLIT - 1) / SPLIT;
+  const int64_t c_begin = slice * slice_len;
+  const int64_t c_end = c_begin + slice_len < KV ? c_begin + slice_len : KV;
 
   // Weight rows of this wave.
   const uint4* wrow[NR];
@@ -97,45 +82,154 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
     }
   }
 
-  // Issue the first weight loads before the prologue: they do not depend on x.
+  // x (and the norm weight) first: the waits below are in issue order, so
+  // loads issued before the weight stream come back without waiting for it.
+  constexpr int kXReg = 8;  // x vectors per thread held in registers
+  const bool aligned = a.n[22] != 0;
+  const uint4* xg0 = static_cast<const uint4*>(a.p[0]);
+  const int64_t xrow0 = a.n[2] / V;
+  const int64_t x_per_thread = (KV + 255) / 256;
+  const bool x_in_regs = STAGE && aligned && M * x_per_thread <= kXReg &&
+                         (!PRO || (a.n[19] == dt && x_per_thread <= 4));
+  uint4 xreg[kXReg];
+  uint4 nreg[4];
+  if (x_in_regs) {
+#pragma unroll
+    for (int i = 0; i < kXReg; ++i) {
+      const int64_t m = i / x_per_thread, c = threadIdx.x + 256 * (i % x_per_thread);
+      xreg[i] = (m < M && c < KV) ? xg0[m * xrow0 + c] : make_uint4(0, 0, 0, 0);
+    }
+    if (PRO) {
+      const uint4* nw = static_cast<const uint4*>(a.p[1]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t c = threadIdx.x + 256 * i;
+        nreg[i] = (i < x_per_thread && c < KV) ? nw[c] : make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+
+  // The weight stream: it does not depend on x.
   uint4 wv[U][NR];
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const int64_t c = lane + 64 * u;
-      wv[u][r] = (valid[r] && c < KV) ? wrow[r][c] : make_uint4(0, 0, 0, 0);
+      const int64_t c = c_begin + lane + 64 * u;
+      wv[u][r] = (valid[r] && c < c_end) ? wrow[r][c] : make_uint4(0, 0, 0, 0);
+    }
+
+  // Residual values this lane writes later: load them now, off the critical path.
+  float resv[MM][NR];
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      resv[m][r] = 0.f;
+      if (!SILU && m < M && valid[r] && a.p[10 + seg[r]])
+        resv[m][r] = E::to_f(static_cast<const T*>(a.p[10 + seg[r]])[m * a.n[15 + seg[r]] + idx[r]]);
     }
 
   T* xs_t = reinterpret_cast<T*>(xs);
-  if (STAGE) {
-    if (PRO) {
-      const int wdt = static_cast<int>(a.n[19]);
-      for (int m = 0; m < M; ++m) {
-        float ss = 0.f;
-        for (int64_t k = threadIdx.x; k < K; k += 256) {
-          const float x = load_f(a.p[0], m * a.n[2] + k, dt);
-          ss += E::round(x * x);
+  if (STAGE && x_in_regs) {
+    // rounded squares per row, then the normalised row into LDS
+    float ss[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) ss[m] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kXReg; ++i) {
+      const int64_t m = i / x_per_thread, c = threadIdx.x + 256 * (i % x_per_thread);
+      if (m < M && c < KV) {
+        if (PRO) {
+          float f[V];
+          unpack<T>(xreg[i], f);
+          float part = 0.f;
+#pragma unroll
+          for (int e = 0; e < V; ++e) part += E::round(f[e] * f[e]);
+#pragma unroll
+          for (int mm = 0; mm < MM; ++mm)
+            if (mm == m) ss[mm] += part;
+        } else {
+          xs[m * KV + c] = xreg[i];
         }
+      }
+    }
+    if (PRO) {
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        if (m >= M) break;
+        const float total = E::round(block_sum256(ss[m], red));
+        if (threadIdx.x == 0) {
+          const float mean = E::round(total / E::round(static_cast<float>(K)));
+          rnorm[m] = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kXReg; ++i) {
+        const int64_t m = i / x_per_thread, q = i % x_per_thread, c = threadIdx.x + 256 * q;
+        if (m < M && c < KV) {
+          float f[V], w[V];
+          unpack<T>(xreg[i], f);
+          uint4 wn = nreg[0];
+#pragma unroll
+          for (int qq = 1; qq < 4; ++qq)
+            if (qq == q) wn = nreg[qq];
+          unpack<T>(wn, w);
+          const float r = rnorm[m];
+#pragma unroll
+          for (int e = 0; e < V; ++e) f[e] = E::round(E::round(f[e] / r) * w[e]);
+          xs[m * KV + c] = pack<T>(f);
+        }
+      }
+    }
+    __syncthreads();
+  } else if (STAGE) {
+    // Copy x into LDS (16-byte vectors when rows are aligned) and, for the
+    // RMSNorm prologue, accumulate the rounded squares on the way.
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      if (m >= M) break;
+      float ss = 0.f;
+      if (aligned) {
+        for (int64_t c = threadIdx.x; c < KV; c += 256) {
+          const uint4 v = xg0[m * xrow0 + c];
+          xs[m * KV + c] = v;
+          if (PRO) {
+            float f[V];
+            unpack<T>(v, f);
+#pragma unroll
+            for (int e = 0; e < V; ++e) ss += E::round(f[e] * f[e]);
+          }
+        }
+      } else {
+        for (int64_t k = threadIdx.x; k < K; k += 256) {
+          const T v = static_cast<const T*>(a.p[0])[m * a.n[2] + k];
+          xs_t[m * K + k] = v;
+          if (PRO) {
+            const float f = E::to_f(v);
+            ss += E::round(f * f);
+          }
+        }
+      }
+      if (PRO) {
         ss = E::round(block_sum256(ss, red));
         if (threadIdx.x == 0) {
           const float mean = E::round(ss / E::round(static_cast<float>(K)));
           rnorm[m] = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
         }
       }
-      __syncthreads();
-      for (int64_t e = threadIdx.x; e < M * K; e += 256) {
-        const int64_t m = e / K, k = e - m * K;
-        const float x = load_f(a.p[0], m * a.n[2] + k, dt);
-        xs_t[e] = E::from_f(E::round(E::round(x / rnorm[m]) * load_f(a.p[1], k, wdt)));
-      }
-    } else {
-      for (int64_t e = threadIdx.x; e < M * K; e += 256) {
-        const int64_t m = e / K, k = e - m * K;
-        xs_t[e] = static_cast<const T*>(a.p[0])[m * a.n[2] + k];
-      }
     }
     __syncthreads();
+    if (PRO) {
+      const int wdt = static_cast<int>(a.n[19]);
+      for (int64_t e = threadIdx.x; e < M * K; e += 256) {
+        const int64_t m = e / K, k = e - m * K;
+        const float x = E::to_f(xs_t[e]);
+        xs_t[e] = E::from_f(E::round(E::round(x / rnorm[m]) * load_f(a.p[1], k, wdt)));
+      }
+      __syncthreads();
+    }
   }
 
   const int64_t nwaves = SILU ? a.n[7] : 0;
@@ -143,7 +237,7 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
 #pragma unroll
   for (int r = 0; r < NR; ++r) any = any || valid[r];
   (void)nwaves;
-  if (!any) return;
+  if (SPLIT == 1 && !any) return;
 
   float acc[MM][NR];
 #pragma unroll
@@ -153,11 +247,11 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
 
   const uint4* xg = static_cast<const uint4*>(a.p[0]);
   const int64_t xrow = a.n[2] / V;
-  for (int64_t c0 = lane; c0 < KV; c0 += 64 * U) {
+  for (int64_t c0 = c_begin + lane; c0 < c_end; c0 += 64 * U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + 64 * u;
-      if (c < KV) {
+      if (c < c_end) {
         float wf[NR][V];
 #pragma unroll
         for (int r = 0; r < NR; ++r) unpack<T>(wv[u][r], wf[r]);
@@ -178,7 +272,7 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
       const int64_t cn = c + 64 * U;
 #pragma unroll
       for (int r = 0; r < NR; ++r)
-        wv[u][r] = (valid[r] && cn < KV) ? wrow[r][cn] : make_uint4(0, 0, 0, 0);
+        wv[u][r] = (valid[r] && cn < c_end) ? wrow[r][cn] : make_uint4(0, 0, 0, 0);
     }
   }
 
@@ -187,6 +281,26 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[m][r] = wave_sum(acc[m][r]);
 
+  if (SPLIT > 1) {
+    // combine the K slices of each row group through LDS
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) partial[wave_in_block][m][r] = acc[m][r];
+    }
+    __syncthreads();
+    if (slice != 0 || !any) return;
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        float total = 0.f;
+#pragma unroll
+        for (int q = 0; q < SPLIT; ++q) total += partial[wave_in_block + q][m][r];
+        acc[m][r] = total;
+      }
+  }
   if (lane != 0) return;
   for (int m = 0; m < M; ++m) {
     if (SILU) {
@@ -202,32 +316,37 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
         if (!valid[r]) continue;
         const int s = seg[r];
         float y = E::round(acc[m][r]);
-        if (a.p[10 + s]) {
-          const float res = E::to_f(static_cast<const T*>(a.p[10 + s])[m * a.n[15 + s] + idx[r]]);
-          y = E::round(res + y);
-        }
+        if (a.p[10 + s]) y = E::round(resv[m][r] + y);
         static_cast<T*>(a.p[6 + s])[m * a.n[11 + s] + idx[r]] = E::from_f(y);
       }
     }
   }
 }
 
-template <typename T, int MM, int NR, int U>
+template <typename T, int MM, int NR, int U, int SPLIT>
 const void* pick(bool pro, bool silu, bool stage) {
   if (silu) {
-    if (pro) return reinterpret_cast<const void*>(&k_gemv<T, MM, 2, U, true, true, true>);
-    return stage ? reinterpret_cast<const void*>(&k_gemv<T, MM, 2, U, false, true, true>)
-                 : reinterpret_cast<const void*>(&k_gemv<T, MM, 2, U, false, true, false>);
+    if (pro) return reinterpret_cast<const void*>(&k_gemv<T, MM, 2, U, true, true, true, SPLIT>);
+    return stage ? reinterpret_cast<const void*>(&k_gemv<T, MM, 2, U, false, true, true, SPLIT>)
+                 : reinterpret_cast<const void*>(&k_gemv<T, MM, 2, U, false, true, false, SPLIT>);
   }
-  if (pro) return reinterpret_cast<const void*>(&k_gemv<T, MM, NR, U, true, false, true>);
-  return stage ? reinterpret_cast<const void*>(&k_gemv<T, MM, NR, U, false, false, true>)
-               : reinterpret_cast<const void*>(&k_gemv<T, MM, NR, U, false, false, false>);
+  if (pro) return reinterpret_cast<const void*>(&k_gemv<T, MM, NR, U, true, false, true, SPLIT>);
+  return stage ? reinterpret_cast<const void*>(&k_gemv<T, MM, NR, U, false, false, true, SPLIT>)
+               : reinterpret_cast<const void*>(&k_gemv<T, MM, NR, U, false, false, false, SPLIT>);
 }
 
 template <typename T>
-const void* pick_rows(int64_t m, bool pro, bool silu, bool stage) {
-  if (m == 1) return pick<T, 1, 1, 4>(pro, silu, stage);
-  return pick<T, kMaxRows, 2, 2>(pro, silu, stage);
+const void* pick_rows(int64_t m, int64_t kv, bool pro, bool silu, bool stage) {
+  // U = 16-byte vectors per lane in flight per row: enough for one round
+  // trip over the whole row where registers allow.
+  const int64_t per_lane = (kv + 63) / 64;
+  if (m == 1) {
+    if (per_lane <= 4) return pick<T, 1, 1, 4, 1>(pro, silu, stage);
+    if (per_lane <= 8) return pick<T, 1, 1, 8, 1>(pro, silu, stage);
+    return pick<T, 1, 1, 12, 1>(pro, silu, stage);
+  }
+  if (per_lane <= 4) return pick<T, kMaxRows, 2, 4, 1>(pro, silu, stage);
+  return pick<T, kMaxRows, 2, 8, 1>(pro, silu, stage);
 }
 
 const char* plan_gemv(KArgs& a, Launch& l) {
@@ -251,13 +370,18 @@ const char* plan_gemv(KArgs& a, Launch& l) {
     rows += a.n[7 + s];
   }
   const int nr = M == 1 ? 1 : 2;
-  const int64_t waves = silu ? a.n[7] : (rows + nr - 1) / nr;
-  const int64_t blocks = (waves + 3) / 4;
+  // n[21]: waves sharing one row group (K split), 0 = automatic.  Small
+  // matrices split K to keep more loads in flight per CU.
+  int64_t split = a.n[21] == 0 ? 1 : a.n[21];
+  const int64_t groups = silu ? a.n[7] : (rows + nr - 1) / nr;
+  if (split != 1) return "gemv: only split 1 is built";
+  const int64_t per_block = 4 / split;
+  const int64_t blocks = (groups + per_block - 1) / per_block;
   if (blocks > 2147483647) return "gemv: too many rows";
   switch (dt) {
-    case F32: l.func = pick_rows<float>(M, pro, silu, stage); break;
-    case F16: l.func = pick_rows<__half>(M, pro, silu, stage); break;
-    default: l.func = pick_rows<bf16_t>(M, pro, silu, stage); break;
+    case F32: l.func = pick_rows<float>(M, K / vec, pro, silu, stage); break;
+    case F16: l.func = pick_rows<__half>(M, K / vec, pro, silu, stage); break;
+    default: l.func = pick_rows<bf16_t>(M, K / vec, pro, silu, stage); break;
   }
   l.grid = dim3(static_cast<unsigned>(blocks));
   l.block = dim3(256);

@@ -43,6 +43,9 @@ class HostDevice:
     def array(self, value):
         return value if isinstance(value, HostArray) else HostArray(np.asarray(value))
 
+    def zeros(self, shape, dtype):
+        return HostArray(np.zeros(shape, dtype))
+
 
 class CpuPlanCompiler(HIPCompiler):
     def __init__(self):  # no library, no GPU
@@ -417,9 +420,63 @@ def s_gemv(mem, p, n, f):
     return 0
 
 
+def s_decode_attn(mem, p, n, f):
+    B, H, KV, C, dt = n[0:5]
+    qs, ks, vs = n[5:8], n[8:11], n[11:14]
+    mode, length = n[14], n[15]
+    cs = n[16:20]
+    wsb, wsc, msb, msh, msc, mdt, wdt, in_place = n[20:28]
+    G = H // KV
+    div = _round(np.float32(f[0]), dt)
+    error = 0
+    d = np.arange(64)
+    newk = {}
+    for b in range(B):
+        pos = int(mem.view(p[3], 3, B if mode == 2 else 1)[b if mode == 2 else 0])
+        if not 0 <= pos < length:
+            error |= 2
+            pos = 0
+        c = load(mem, p[4], dt, pos * 64 + np.arange(32))
+        s = load(mem, p[4], dt, pos * 64 + 32 + np.arange(32))
+
+        def rope(x):
+            return _round(np.concatenate([x[:32] * c + x[32:] * -s, x[:32] * s + x[32:] * c]), dt)
+
+        w = load(mem, p[7], wdt, b * wsb + np.arange(C) * wsc)
+        keep = _round(1 - w, dt)[:, None]
+        for g in range(KV):
+            k = rope(load(mem, p[1], dt, b * ks[0] + g * ks[1] + d * ks[2]))
+            v = load(mem, p[2], dt, b * vs[0] + g * vs[1] + d * vs[2])
+            idx = b * cs[0] + g * cs[1] + np.arange(C)[:, None] * cs[2] + d[None, :] * cs[3]
+            Kc, Vc = load(mem, p[5], dt, idx), load(mem, p[6], dt, idx)
+            Kn = np.where(w[:, None] != 0, _round(_round(Kc * keep, dt) + _round(k[None] * w[:, None], dt), dt), Kc)
+            Vn = np.where(w[:, None] != 0, _round(_round(Vc * keep, dt) + _round(v[None] * w[:, None], dt), dt), Vc)
+            newk[(b, g)] = (idx, Kn, Vn, w)
+            with np.errstate(all="ignore"):
+                for h in range(g * G, (g + 1) * G):
+                    q = rope(load(mem, p[0], dt, b * qs[0] + h * qs[1] + d * qs[2]))
+                    sc = _round(_round((Kn.astype(np.float64) @ q).astype(np.float32), dt) / div, dt)
+                    if p[8][0] >= 0:
+                        sc = _round(sc + load(mem, p[8], mdt, b * msb + h * msh + np.arange(C) * msc), dt)
+                    e = _round(np.exp(_round(sc - sc.max(), dt)), dt)
+                    S = _round(e.sum(), dt)
+                    out = (_round(e / S, dt).astype(np.float64) @ Vn).astype(np.float32)
+                    store(mem, p[9], dt, (b * H + h) * 64 + d, out)
+    for (b, g), (idx, Kn, Vn, w) in newk.items():
+        if in_place:
+            rows = w != 0
+            store(mem, p[10], dt, idx[rows].reshape(-1), Kn[rows].reshape(-1))
+            store(mem, p[11], dt, idx[rows].reshape(-1), Vn[rows].reshape(-1))
+        else:
+            base = ((b * KV + g) * C) * 64
+            store(mem, p[10], dt, base + np.arange(C * 64), Kn.reshape(-1))
+            store(mem, p[11], dt, base + np.arange(C * 64), Vn.reshape(-1))
+    return error
+
+
 STEP = {
     P.K_FILL: s_fill, P.K_COPY: s_copy, P.K_ELEMENTWISE: s_elementwise, P.K_REDUCE: s_reduce,
     P.K_GATHER: s_gather, P.K_MATMUL: s_matmul, P.K_SOFTMAX: s_softmax, P.K_RMSNORM: s_rmsnorm,
     P.K_ROPE: s_rope, P.K_SDPA: s_sdpa, P.K_KV_WRITE: s_kv_write, P.K_KV_PLACE: s_kv_place,
-    P.K_GEMV: s_gemv,
+    P.K_GEMV: s_gemv, P.K_DECODE_ATTN: s_decode_attn,
 }

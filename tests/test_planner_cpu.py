@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from chomikgrad import Tensor, realize, synthetic
-from chomikgrad._planner import K_GEMV, K_KV_PLACE, K_KV_WRITE, K_SDPA, plan_graph
+from chomikgrad._planner import K_DECODE_ATTN, K_GEMV, K_KV_PLACE, K_KV_WRITE, K_SDPA, plan_graph
 from chomikgrad.dtypes import BFLOAT16, bf16_to_float32, to_bf16
 from chomikgrad.llama import (
     LlamaBatchedDecoderStep,
@@ -103,8 +103,9 @@ def test_linear_uses_gemv_with_fusions():
     planned, got = model_run(outputs, leaves + caches, donate=caches)
     kinds = [s.kind for s in planned.steps]
     assert kinds.count(K_GEMV) == 4 * config.num_hidden_layers + 1
-    assert kinds.count(K_KV_WRITE) == 2 * config.num_hidden_layers
-    assert kinds.count(K_SDPA) == config.num_hidden_layers
+    assert kinds.count(K_DECODE_ATTN) == config.num_hidden_layers
+    assert kinds.count(K_KV_WRITE) == 0 and kinds.count(K_SDPA) == 0
+    assert len(kinds) == 5 * config.num_hidden_layers + 2  # gather + per layer 5 + lm_head
     assert "gemv[rms_norm]" in planned.source and "gemv[rms_norm+silu_mul]" in planned.source
     assert "gemv[residual]" in planned.source
     for value, reference in zip(got, expected):

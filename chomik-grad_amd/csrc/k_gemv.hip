@@ -17,6 +17,8 @@
 #include "chip.h"
 #include "chomik_hip.h"
 
+#include <cstdlib>
+
 namespace chip {
 namespace {
 
@@ -323,6 +325,359 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
   }
 }
 
+// Single-row input (M == 1, x 16-byte aligned): the decode shape.  One
+// wavefront per output row (per gate/up pair with SILU); every lane holds the
+// x and weight vectors of columns lane + 64 u in registers, so nothing goes
+// through LDS and the block never synchronises.  Each wave sees all of x, so
+// the RMSNorm prologue is a wave reduction of its own registers.  Loads are
+// issued x first, then the norm weight, then the weight rows, so the norm is
+// computed while the weight stream is still in flight.  Same KArgs layout as
+// k_gemv.
+//
+// Every wave repeats the prologue over all of x, so its arithmetic is kept to
+// a few instructions per element on 32-bit words holding two 16-bit values:
+//  * products rounded to the storage type are single packed fp16 multiplies
+//    (the fp32 product of two fp16 values is exact, so rounding it once to
+//    fp16 equals the correctly rounded fp16 product);
+//  * x / r is x * (1/r) plus one Newton correction (see quotient());
+//  * dot products accumulate in fp32 with v_dot2 (two exact 16-bit products
+//    per instruction).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef short s2v __attribute__((ext_vector_type(2)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 load_w(const uint4* p) {
+  if (NT) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  }
+  return *p;
+}
+
+// Two 16-bit values in one 32-bit word.
+template <typename T> struct Word;
+template <> struct Word<__half> {
+  static constexpr uint32_t kOnes = 0x3c003c00u;
+  __device__ static __forceinline__ float dot(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, a), __builtin_bit_cast(h2v, b), c, false);
+  }
+  __device__ static __forceinline__ uint32_t mul(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, a) * __builtin_bit_cast(h2v, b));
+  }
+  __device__ static __forceinline__ float lo(uint32_t a) { return static_cast<float>(__builtin_bit_cast(h2v, a).x); }
+  __device__ static __forceinline__ float hi(uint32_t a) { return static_cast<float>(__builtin_bit_cast(h2v, a).y); }
+  __device__ static __forceinline__ uint32_t pack(float l, float h) {
+    h2v v;
+    v.x = static_cast<_Float16>(l);
+    v.y = static_cast<_Float16>(h);
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  // the corrected quotient is exact for every finite fp16 x over every
+  // normal fp16 divisor; for a zero, infinite or NaN divisor x * (1 / d) is
+  // itself the IEEE quotient
+  static constexpr bool kNoBranch = true;
+  __device__ static __forceinline__ bool fast_divisor(float d) { return d >= 0x1p-14f && d < 0x1p16f; }
+  __device__ static __forceinline__ bool fast_numerator(float) { return true; }
+};
+template <> struct Word<bf16_t> {
+  static constexpr uint32_t kOnes = 0x3f803f80u;
+  static constexpr bool kNoBranch = false;
+  __device__ static __forceinline__ float dot(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s2v, a), __builtin_bit_cast(s2v, b), c, false);
+  }
+  __device__ static __forceinline__ float lo(uint32_t a) { return __uint_as_float(a << 16); }
+  __device__ static __forceinline__ float hi(uint32_t a) { return __uint_as_float(a & 0xffff0000u); }
+  __device__ static __forceinline__ uint32_t pack(float l, float h) {
+    return static_cast<uint32_t>(f32_to_bf16_bits(l)) | (static_cast<uint32_t>(f32_to_bf16_bits(h)) << 16);
+  }
+  // the bf16 product is exact in fp32; round it once
+  __device__ static __forceinline__ uint32_t mul(uint32_t a, uint32_t b) {
+    return pack(lo(a) * lo(b), hi(a) * hi(b));
+  }
+  __device__ static __forceinline__ bool fast_divisor(float d) { return d >= 0x1p-9f && d <= 0x1p64f; }
+  __device__ static __forceinline__ bool fast_numerator(float x) {
+    const float ax = fabsf(x);
+    return ax == 0.f || (ax >= 0x1p-100f && ax <= 0x1p100f);
+  }
+};
+
+// RN(x / d) from inv = RN(1 / d): q = x * inv, then one Newton correction
+// with the exact residual fma(-q, d, x) (Markstein).  Checked exhaustively on
+// the host against IEEE division followed by rounding to the storage type:
+// every finite fp16 x over every normal fp16 d, and every bf16 x with |x| in
+// [2^-100, 2^100] over every bf16 d in [2^-9, 2^64], with inv off by up to
+// +-2 ulp.  A wave whose divisor or any numerator falls outside those
+// domains divides exactly instead.
+__device__ __forceinline__ float quotient(float x, float d, float inv) {
+  const float q = x * inv;
+  return copysignf(fmaf(fmaf(-q, d, x), inv, q), x);
+}
+
+__device__ __forceinline__ uint4 load_x(const uint4* p) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// FULL: K / vector == 64 * VPL exactly, so every lane loads VPL vectors per
+// row with no masking and one pass covers the row; otherwise the row is
+// walked in chunks of VPL vectors per lane with the tail masked.
+template <typename T, int NR, int VPL, bool FULL, bool PRO, bool SILU, bool NT>
+__global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
+  using E = Elem<T>;
+  constexpr bool kWord = sizeof(T) == 2;
+  constexpr int V = 16 / sizeof(T);
+  const int64_t K = a.n[1];
+  const int KV = static_cast<int>(K / V);
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
+
+  const uint4* wrow[NR];
+  int seg[NR];
+  int64_t idx[NR];
+  bool valid[NR];
+  if (SILU) {
+    const bool ok = wave < a.n[7];
+    wrow[0] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2]) + (ok ? wave : 0) * K);
+    wrow[1] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[3]) + (ok ? wave : 0) * K);
+    seg[0] = 0;
+    seg[1] = 1;
+    idx[0] = idx[1] = wave;
+    valid[0] = valid[1] = ok;
+  } else {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      int64_t g = wave * NR + r;
+      int s = 0;
+      while (s < a.n[4] && g >= a.n[7 + s]) {
+        g -= a.n[7 + s];
+        ++s;
+      }
+      valid[r] = s < a.n[4];
+      seg[r] = valid[r] ? s : 0;
+      idx[r] = valid[r] ? g : 0;
+      wrow[r] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2 + seg[r]]) + idx[r] * K);
+    }
+  }
+  if (!valid[0]) return;  // rows are assigned in order: no valid row after an invalid one
+
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  const uint4* xg = static_cast<const uint4*>(a.p[0]);
+  const uint4* ng = static_cast<const uint4*>(a.p[1]);
+  const int chunks = FULL ? 1 : (KV + 64 * VPL - 1) / (64 * VPL);
+  float acc[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+  // the residual this row's writer adds, loaded ahead of the stream
+  float resv[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    resv[r] = 0.f;
+    if (!SILU && lane == 0 && valid[r] && a.p[10 + seg[r]])
+      resv[r] = E::to_f(static_cast<const T*>(a.p[10 + seg[r]])[idx[r]]);
+  }
+
+  for (int chunk = 0; chunk < chunks; ++chunk) {
+    const int base = chunk * 64 * VPL + lane;
+    uint4 xv[VPL], nv[PRO ? VPL : 1], wv[VPL][NR];
+#pragma unroll
+    for (int u = 0; u < VPL; ++u) {
+      const int c = base + 64 * u;
+      if (FULL) {
+        xv[u] = load_x(xg + c);
+      } else {
+        const uint4 v = load_x(xg + (c < KV ? c : KV - 1));
+        xv[u] = c < KV ? v : zero;
+      }
+    }
+    if (PRO) {
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const int c = base + 64 * u;
+        if (FULL) {
+          nv[u] = load_x(ng + c);
+        } else {
+          const uint4 v = load_x(ng + (c < KV ? c : KV - 1));
+          nv[u] = c < KV ? v : zero;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VPL; ++u)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int c = base + 64 * u;
+        if (FULL) {
+          wv[u][r] = load_w<NT>(wrow[r] + c);
+        } else {
+          const uint4 v = load_w<NT>(wrow[r] + (c < KV ? c : KV - 1));
+          wv[u][r] = c < KV ? v : zero;
+        }
+      }
+    // rows of an invalid slot (NR > 1 tail) read row 0 of their segment and
+    // contribute nothing: their results are never stored
+
+    if constexpr (kWord) {
+      using W = Word<T>;
+      uint32_t xw[VPL][4];
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        xw[u][0] = xv[u].x;
+        xw[u][1] = xv[u].y;
+        xw[u][2] = xv[u].z;
+        xw[u][3] = xv[u].w;
+      }
+      if (PRO) {
+        // the planner admits the prologue only when one chunk covers K
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < VPL; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[u][i], xw[u][i]), W::kOnes, ss);
+        const float total = E::round(wave_sum(ss));
+        const float mean = E::round(total / E::round(static_cast<float>(K)));
+        const float rn = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+        const float inv = 1.0f / rn;
+        if constexpr (W::kNoBranch) {
+          const bool corrected = W::fast_divisor(rn);
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) {
+            const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float lo = W::lo(xw[u][i]), hi = W::hi(xw[u][i]);
+              const float ql = corrected ? quotient(lo, rn, inv) : lo * inv;
+              const float qh = corrected ? quotient(hi, rn, inv) : hi * inv;
+              xw[u][i] = W::mul(W::pack(ql, qh), nw[i]);
+            }
+          }
+        } else {
+          bool fast = W::fast_divisor(rn);
+#pragma unroll
+          for (int u = 0; u < VPL; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              fast = fast && W::fast_numerator(W::lo(xw[u][i])) && W::fast_numerator(W::hi(xw[u][i]));
+          if (__all(fast)) {
+#pragma unroll
+            for (int u = 0; u < VPL; ++u) {
+              const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                xw[u][i] = W::mul(W::pack(quotient(W::lo(xw[u][i]), rn, inv), quotient(W::hi(xw[u][i]), rn, inv)), nw[i]);
+            }
+          } else {
+#pragma unroll
+            for (int u = 0; u < VPL; ++u) {
+              const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                xw[u][i] = W::mul(W::pack(W::lo(xw[u][i]) / rn, W::hi(xw[u][i]) / rn), nw[i]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const uint32_t ww[4] = {wv[u][r].x, wv[u][r].y, wv[u][r].z, wv[u][r].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[r] = W::dot(xw[u][i], ww[i], acc[r]);
+        }
+      }
+    } else {
+      float xf[VPL][V];
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) unpack<T>(xv[u], xf[u]);
+      if (PRO) {
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < VPL; ++u)
+#pragma unroll
+          for (int e = 0; e < V; ++e) ss += xf[u][e] * xf[u][e];
+        const float total = wave_sum(ss);
+        const float rn = sqrtf(total / static_cast<float>(K) + a.f[0]);
+#pragma unroll
+        for (int u = 0; u < VPL; ++u) {
+          float w[V];
+          unpack<T>(nv[u], w);
+#pragma unroll
+          for (int e = 0; e < V; ++e) xf[u][e] = xf[u][e] / rn * w[e];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < VPL; ++u)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          float wf[V];
+          unpack<T>(wv[u][r], wf);
+#pragma unroll
+          for (int e = 0; e < V; ++e) acc[r] = fmaf(xf[u][e], wf[e], acc[r]);
+        }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane != 0) return;
+  if (SILU) {
+    const float g = E::round(acc[0]);
+    const float u = E::round(acc[1]);
+    const float denom = E::round(E::round(expf(-g)) + 1.f);
+    static_cast<T*>(a.p[6])[idx[0]] = E::from_f(E::round(E::round(g / denom) * u));
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (!valid[r]) continue;
+    const int s = seg[r];
+    float y = E::round(acc[r]);
+    if (a.p[10 + s]) y = E::round(resv[r] + y);
+    static_cast<T*>(a.p[6 + s])[idx[r]] = E::from_f(y);
+  }
+}
+
+template <typename T, int VPL, bool FULL, bool NT>
+const void* pick_row_kernel(bool pro, bool silu) {
+  if (silu) {
+    return pro ? reinterpret_cast<const void*>(&k_gemv_row<T, 2, VPL, FULL, true, true, NT>)
+               : reinterpret_cast<const void*>(&k_gemv_row<T, 2, VPL, FULL, false, true, NT>);
+  }
+  return pro ? reinterpret_cast<const void*>(&k_gemv_row<T, 1, VPL, FULL, true, false, NT>)
+             : reinterpret_cast<const void*>(&k_gemv_row<T, 1, VPL, FULL, false, false, NT>);
+}
+
+template <typename T, bool NT>
+const void* pick_row_nt(int64_t kv, bool pro, bool silu) {
+  // exact fits of the decode shapes: 512, 1024, 2048, 4096, 5632, 8192
+  // 16-bit columns (and 256, 512, 1024, 2048 float32 ones)
+  if (kv % 64 == 0) {
+    switch (kv / 64) {
+      case 1: return pick_row_kernel<T, 1, true, NT>(pro, silu);
+      case 2: return pick_row_kernel<T, 2, true, NT>(pro, silu);
+      case 4: return pick_row_kernel<T, 4, true, NT>(pro, silu);
+      case 8: return pick_row_kernel<T, 8, true, NT>(pro, silu);
+      case 11: if (!silu) return pick_row_kernel<T, 11, true, NT>(pro, silu); break;
+      case 16: if (!silu && !pro) return pick_row_kernel<T, 16, true, NT>(pro, silu); break;
+      default: break;
+    }
+  }
+  return pick_row_kernel<T, 4, false, NT>(pro, silu);
+}
+
+template <typename T>
+const void* pick_row(int64_t kv, bool pro, bool silu, bool nt) {
+  return nt ? pick_row_nt<T, true>(kv, pro, silu) : pick_row_nt<T, false>(kv, pro, silu);
+}
+
+// Tuning knobs read once: waves per block of the row kernel (0 = by size)
+// and non-temporal weight loads.
+int env_int(const char* name, int fallback) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : fallback;
+}
+
 template <typename T, int MM, int NR, int U, int SPLIT>
 const void* pick(bool pro, bool silu, bool stage) {
   if (silu) {
@@ -368,6 +723,33 @@ const char* plan_gemv(KArgs& a, Launch& l) {
   for (int s = 0; s < segs; ++s) {
     if (a.n[7 + s] <= 0) return "gemv: empty segment";
     rows += a.n[7 + s];
+  }
+  const int64_t kv = K / vec;
+  const bool aligned = a.n[22] != 0;
+  // the prologue needs the whole row in one pass: an exact fit of 1, 2, 4,
+  // 8 (or 11 without SiLU) vectors per lane, or at most 4 with the tail masked
+  const int64_t per_lane = (kv + 63) / 64;
+  const bool one_pass = (kv % 64 == 0 && (per_lane == 1 || per_lane == 2 || per_lane == 4 ||
+                                          per_lane == 8 || (per_lane == 11 && !silu))) ||
+                        per_lane <= 4;
+  const bool row_ok = M == 1 && aligned && (!pro || (a.n[19] == dt && one_pass));
+  if (row_ok) {
+    static const int waves_knob = env_int("CHOMIK_HIP_GEMV_WAVES", 0);
+    static const int nt_knob = env_int("CHOMIK_HIP_GEMV_NT", 1);
+    const int64_t groups = silu ? a.n[7] : rows;
+    const int64_t waves = waves_knob > 0 ? waves_knob : (groups >= 4096 ? 4 : 1);
+    if (waves < 1 || waves > 4) return "gemv: CHOMIK_HIP_GEMV_WAVES must be 1..4";
+    const int64_t blocks = (groups + waves - 1) / waves;
+    if (blocks > 2147483647) return "gemv: too many rows";
+    switch (dt) {
+      case F32: l.func = pick_row<float>(kv, pro, silu, nt_knob != 0); break;
+      case F16: l.func = pick_row<__half>(kv, pro, silu, nt_knob != 0); break;
+      default: l.func = pick_row<bf16_t>(kv, pro, silu, nt_knob != 0); break;
+    }
+    l.grid = dim3(static_cast<unsigned>(blocks));
+    l.block = dim3(static_cast<unsigned>(64 * waves));
+    l.shmem = 0;
+    return nullptr;
   }
   const int nr = M == 1 ? 1 : 2;
   // n[21]: waves sharing one row group (K split), 0 = automatic.  Small

@@ -10,10 +10,12 @@ caches are donated and updated in place; token, position and masks advance
 on the device; no host round trip per token).
 
 Besides the JSON line's ``value`` (decode tok/s), ``roofline`` describes the
-dominant kernel -- the fused RMSNorm + gate/up GEMV + SiLU -- from per-launch
-HIP-event timings of the real decode plan, and ``cpu_baseline`` times the
-NumPy oracle (the reference's cpu plugin algorithm) on a bounded sample of
-the same workload on this host.
+dominant kernel (the largest share of decode time per token) from HIP-event
+timings of the real decode plan's launches, with the HBM traffic per launch
+measured by FETCH_SIZE/WRITE_SIZE counter runs (profiles/decode_c2_traffic.json,
+when it lists that kernel), and ``cpu_baseline`` times the NumPy oracle (the
+reference's cpu plugin algorithm) on a bounded sample of the same workload on
+this host.
 """
 
 from __future__ import annotations
@@ -42,6 +44,7 @@ def log(message: str) -> None:
 
 
 def kernel_label(step) -> str:
+    """Kernel kind, its fusions and (for GEMVs) the weight shape N x K."""
     from chomikgrad._planner import K_GEMV, KIND_NAMES
 
     if step.kind != K_GEMV:
@@ -53,14 +56,21 @@ def kernel_label(step) -> str:
         tags.append("silu_mul")
     if any(s["res"] is not None for s in step.attrs["segments"]):
         tags.append("residual")
-    return "gemv[" + "+".join(tags) + "]" if tags else "gemv"
+    rows = sum(seg["w"].shape[0] for seg in step.attrs["segments"])
+    shape = f" {rows}x{step.attrs['K']}"
+    return ("gemv[" + "+".join(tags) + "]" if tags else "gemv") + shape
 
 
 def algorithmic_bytes(step) -> int:
     """Bytes a kernel must move at minimum: every operand read once, every
     result written once (KV writes in place touch one row per head)."""
-    from chomikgrad._planner import K_GEMV, K_KV_WRITE
+    from chomikgrad._planner import K_GATHER, K_GEMV, K_KV_WRITE
 
+    if step.kind == K_GATHER:
+        # the gathered rows (read once, written once) and the indices
+        table, ids = step.ins[0], step.ins[1]
+        out = step.outs[0]
+        return 2 * out.size * out.itemsize + ids.size * ids.itemsize
     if step.kind == K_GEMV:
         total = sum(pv.size * pv.itemsize for pv in step.reads())
         return total + sum(pv.size * pv.itemsize for pv in {id(o.storage): o for o in step.outs}.values())
@@ -130,7 +140,11 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=115)
     parser.add_argument("--warmup", type=int, default=8)
-    parser.add_argument("--timing-runs", type=int, default=4, help="decode steps timed per kernel")
+    parser.add_argument("--timing-runs", type=int, default=4, help="spare context rows for the kernel timing")
+    parser.add_argument("--timing-rounds", type=int, default=10,
+                        help="round-robin passes over each kernel's per-layer instances")
+    parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                        help="only copy a MIB-sized device buffer three times (counter calibration) and exit")
     parser.add_argument("--cpu-steps", type=int, default=3, help="oracle decode steps for the CPU baseline")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     args = parser.parse_args()
@@ -150,6 +164,16 @@ def main() -> int:
     hip = get_compiler("hip")
     device = hip.device
     log(f"device {device.info}")
+    if args.copy_probe:
+        # A plain device-to-device copy of known size: the reference point
+        # for scaling FETCH_SIZE / WRITE_SIZE counters to bytes.
+        nbytes = args.copy_probe << 20
+        source = device.zeros((nbytes // 2,), np.float16)
+        for _ in range(3):
+            device.copy(source)
+        device.synchronize()
+        print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}), flush=True)
+        return 0
     started = time.perf_counter()
     host = synthetic.host_weights(config, dtype, seed=0)
     weights = synthetic.weights_as_tensors(host)
@@ -212,31 +236,38 @@ def main() -> int:
     tokens = device.to_numpy(history).tolist()
     log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, events {gpu_ms.value:.2f} ms")
 
-    # Per-kernel durations of the same decode plan (direct launches bracketed
-    # by HIP events on the library stream), a few steps further on.
+    # Per-kernel durations of the same decode plan: every step of one kind
+    # and shape (its per-layer instances, round-robin so no cache holds the
+    # repeats) launched back to back between one HIP event pair on the
+    # library stream.  The caches are donated (updated in place), so repeats
+    # of the attention step rewrite the same rows with the same values.
     steps = program._planned.steps
-    durations = {}
-    byte_counts = {}
-    for _ in range(args.timing_runs):
-        ms = (ctypes.c_float * len(steps))()
-        # same slots as the timed loop (already bound): one more decode step
-        lib.call("chip_plan_time_steps", program._plan, ms, ctypes.c_int64(len(steps)))
-        device.greedy_advance(logits_out, token, history=None, step=0, position=position,
-                              attention_mask=attention, write_mask=write, cache_length=context)
-        for step, value in zip(steps, ms):
-            label = kernel_label(step)
-            durations.setdefault(label, []).append(value)
-            byte_counts.setdefault(label, []).append(algorithmic_bytes(step))
+    groups = {}
+    for index, step in enumerate(steps):
+        groups.setdefault(kernel_label(step), []).append(index)
+    breakdown = {}
+    for label, indices in groups.items():
+        ids = (ctypes.c_int64 * len(indices))(*indices)
+        ms = ctypes.c_float(0.0)
+        lib.call("chip_plan_time_repeat", program._plan, ids, ctypes.c_int64(len(indices)),
+                 ctypes.c_int64(args.timing_rounds), ctypes.byref(ms))
+        per_launch_bytes = statistics.mean(algorithmic_bytes(steps[i]) for i in indices)
+        breakdown[label] = {
+            "launches_per_token": len(indices),
+            "avg_us": round(1e3 * ms.value, 3),
+            "us_per_token": round(1e3 * ms.value * len(indices), 2),
+            "bytes_per_launch": int(per_launch_bytes),
+            "gbps": round(per_launch_bytes / (ms.value * 1e-3) / 1e9, 1),
+        }
     device.synchronize()
-    breakdown = {
-        label: {"launches_per_token": len(values) // args.timing_runs,
-                "avg_us": round(1e3 * statistics.mean(values), 3),
-                "us_per_token": round(1e3 * sum(values) / args.timing_runs, 2),
-                "gbps": round(statistics.mean(byte_counts[label]) / (statistics.mean(values) * 1e-3) / 1e9, 1)}
-        for label, values in durations.items()
-    }
     dominant = max(breakdown, key=lambda k: breakdown[k]["us_per_token"])
-    dom_bytes = statistics.mean(byte_counts[dominant])
+    traffic = None
+    traffic_file = ROOT / "profiles" / "decode_c2_traffic.json"
+    if traffic_file.exists():
+        measured = json.loads(traffic_file.read_text()).get("kernels", {}).get(dominant)
+        if measured:
+            traffic = measured["hbm_bytes_per_launch"]
+    dom_bytes = breakdown[dominant]["bytes_per_launch"]
     dom_us = breakdown[dominant]["avg_us"]
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
 
@@ -272,7 +303,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
             "kernel": dominant, "bytes_per_launch": int(dom_bytes), "avg_launch_us": dom_us,
         },
         "cpu_baseline": baseline,

@@ -50,6 +50,8 @@ SIGNATURES = {
     "chip_plan_run": [ctypes.c_void_p],
     "chip_plan_info": [ctypes.c_void_p, c_int64_p, c_int64_p],
     "chip_plan_time_steps": [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.c_int64],
+    "chip_plan_time_repeat": [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int64, ctypes.c_int64,
+                              ctypes.POINTER(ctypes.c_float)],
     "chip_plan_destroy": [ctypes.c_void_p],
     "chip_argmax": [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, c_int64_p],
     "chip_greedy_advance": [

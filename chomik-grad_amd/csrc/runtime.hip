@@ -580,6 +580,42 @@ int chip_plan_time_steps(chip_plan* plan, float* ms_out, int64_t capacity) {
   return check_errors_now();
 }
 
+int chip_plan_time_repeat(chip_plan* plan, const int64_t* steps, int64_t n, int64_t rounds, float* ms_out) {
+  NEED_INIT();
+  if (!plan || !steps || !ms_out || n <= 0 || rounds <= 0) return fail(CHIP_EINVAL, "bad timing arguments");
+  for (int64_t i = 0; i < n; ++i)
+    if (steps[i] < 0 || steps[i] >= static_cast<int64_t>(plan->steps.size()))
+      return fail(CHIP_EINVAL, "step index %lld out of range", static_cast<long long>(steps[i]));
+  for (size_t s = 0; s < plan->slots.size(); ++s) {
+    if (!plan->slot_dirty[s]) continue;
+    for (int user : plan->users[s]) plan->steps[static_cast<size_t>(user)].dirty = true;
+    plan->slot_dirty[s] = 0;
+  }
+  for (Step& step : plan->steps) {
+    if (!step.dirty) continue;
+    int rc = resolve(plan, step);
+    if (rc) return rc;
+  }
+  hipEvent_t start, stop;
+  HIP_TRY(hipEventCreate(&start));
+  HIP_TRY(hipEventCreate(&stop));
+  HIP_TRY(hipEventRecord(start, g_stream));
+  for (int64_t r = 0; r < rounds; ++r)
+    for (int64_t i = 0; i < n; ++i) {
+      Step& step = plan->steps[static_cast<size_t>(steps[i])];
+      HIP_TRY(hipLaunchKernel(step.launch.func, step.launch.grid, step.launch.block, step.params,
+                              step.launch.shmem, g_stream));
+    }
+  HIP_TRY(hipEventRecord(stop, g_stream));
+  HIP_TRY(hipEventSynchronize(stop));
+  float ms = 0.f;
+  HIP_TRY(hipEventElapsedTime(&ms, start, stop));
+  *ms_out = ms / static_cast<float>(n * rounds);
+  (void)hipEventDestroy(start);
+  (void)hipEventDestroy(stop);
+  return check_errors_now();
+}
+
 int chip_plan_destroy(chip_plan* plan) {
   if (!plan) return CHIP_OK;
   if (g_device >= 0) (void)hipStreamSynchronize(g_stream);

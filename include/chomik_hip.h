@@ -140,6 +140,12 @@ int chip_plan_info(chip_plan* plan, int64_t* n_steps, int64_t* arena_bytes);
  * library stream; waits, then writes each step's duration in milliseconds to
  * ms_out[0 .. min(n_steps, capacity) - 1]. */
 int chip_plan_time_steps(chip_plan* plan, float* ms_out, int64_t capacity);
+/* Measurement only (no reference counterpart): launch steps[0 .. n-1] in
+ * order, that sequence ``rounds`` times, back to back on the library stream
+ * between one HIP event pair; waits, then writes the mean duration of one
+ * launch in milliseconds to *ms_out.  Round-robin over the per-layer
+ * instances of a kernel keeps a cache from serving the repeats. */
+int chip_plan_time_repeat(chip_plan* plan, const int64_t* steps, int64_t n, int64_t rounds, float* ms_out);
 int chip_plan_destroy(chip_plan* plan);
 
 /* -- sampling -----------------------------------------------------------------

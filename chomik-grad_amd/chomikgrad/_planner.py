@@ -408,6 +408,13 @@ class Emitter:
         self.steps.append(step)
         return step
 
+    def copy_dense(self, pv: PV) -> PV:
+        """A fresh contiguous, 256-byte aligned copy of ``pv``."""
+        out = self.new_value(pv.shape, pv.dtype, "materialized")
+        if out.size:
+            self.add(K_COPY, [pv], [out])
+        return out
+
     def materialize(self, pv: PV) -> PV:
         if pv.contiguous():
             return pv
@@ -609,7 +616,19 @@ class Emitter:
             and x.row_stride() is not None
         )
         if not fits:
-            return self.matmul(node, x, transposed)
+            gemm = (
+                x.dtype == w.dtype == node.dtype and is_float(x.dtype) and x.itemsize == 2
+                and K % 8 == 0 and w.contiguous() and (w.offset * w.itemsize) % 16 == 0
+                and rows > 0 and w.shape[0] > 0
+            )
+            if not gemm:
+                return self.matmul(node, x, transposed)
+            stride = x.row_stride()
+            if stride is None or stride % 8 or (x.offset * x.itemsize) % 16:
+                x = self.copy_dense(x)
+            out = self.new_value(node.shape, node.dtype, "linear")
+            self.add(K_GEMM, [x, w], [out], rows=rows, K=K, N=w.shape[0])
+            return out
         out = self.new_value(node.shape, node.dtype, "linear")
         stage = rows * K * x.itemsize <= GEMV_STAGE_BYTES
         if not stage and (x.row_stride() % vector or (x.offset * x.itemsize) % 16):
@@ -1103,6 +1122,11 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
                  1 if a["in_place"] else 0]
         ptrs = [_ptr(pv) for pv in (q, k, v, position, table, cache_k, cache_v, w, mask, out, out_k, out_v, tickets)]
         return kind, ptrs, ints, [a["divisor"]]
+    if kind == K_GEMM:
+        x, w = step.ins
+        out = step.outs[0]
+        return kind, [_ptr(x), _ptr(w), _ptr(out)], [
+            a["rows"], a["N"], a["K"], dtype_code(x.dtype), x.row_stride(), w.strides[0], a["N"]], []
     if kind == K_GEMV:
         segments = a["segments"]
         prologue = a["prologue"]

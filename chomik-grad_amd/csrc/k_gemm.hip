@@ -1,0 +1,183 @@
+// MFMA GEMM for prefill linear layers: C[m, n] = sum_k A[m, k] W[n, k]
+// (the IR's MATMUL(x, PERMUTE(W, (1, 0))), llama.py _linear, with x holding
+// many rows), fp16 or bf16 in, fp32 accumulation, one rounding to the output
+// dtype -- the result np.matmul gives for half-precision operands.
+//
+// Both operands are k-contiguous (A row-major with row stride lda, W in its
+// HF (out, in) layout), so every lane loads 16-byte vectors along k.  A block
+// of 256 threads (2 x 2 wavefronts) computes a BM x BN tile with
+// v_mfma_f32_16x16x32 steps; A and W tiles of BK = 64 columns go through a
+// double-buffered LDS stage (rows padded by 16 bytes so the 16 rows a
+// fragment read touches fall in distinct banks), one barrier per stage, the
+// next stage's global loads in flight during the current stage's MFMAs.
+//
+// MFMA 16x16x32 lane layout (lane l, i = l % 16, g = l / 16): the A operand
+// is row i of the A tile, the B operand row i of the W tile, each eight k
+// values (any split of k over the four groups works as long as A and B use
+// the same one; here group g takes k = 8g .. 8g + 7); lane l receives
+// D[4g + r][i], r = 0..3.
+//
+// Blocks are assigned to tiles XCD by XCD: hardware dispatches block b to
+// XCD b % 8, and tile t = (b % 8) * ceil(T / 8) + b / 8 gives each XCD a
+// contiguous run of row-major tiles, so the A rows a run shares stay in that
+// XCD's L2.
+#include "chip.h"
+#include "chomik_hip.h"
+
+namespace chip {
+namespace {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef __bf16 b8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kBK = 64;            // k columns per LDS stage
+constexpr int kPad = 8;            // elements of padding per LDS row
+constexpr int kRow = kBK + kPad;   // LDS row length (elements)
+
+template <typename T> struct Mfma;
+template <> struct Mfma<__half> {
+  __device__ static __forceinline__ f4v step(const uint4& a, const uint4& b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a), __builtin_bit_cast(h8v, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<bf16_t> {
+  __device__ static __forceinline__ f4v step(const uint4& a, const uint4& b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8v, a), __builtin_bit_cast(b8v, b), c, 0, 0, 0);
+  }
+};
+
+// p[0] A, p[1] W, p[2] C.
+// n[0] M, n[1] N, n[2] K, n[3] dtype, n[4] lda, n[5] ldw, n[6] ldc (elements).
+template <typename T, int BM, int BN>
+__global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
+  using E = Elem<T>;
+  constexpr int TM = BM / 2 / 16, TN = BN / 2 / 16;        // 16x16 tiles per wave
+  constexpr int AV = BM * kBK / 8 / 256, WV = BN * kBK / 8 / 256;  // 16-byte vectors per thread
+  static_assert(AV >= 1 && WV >= 1, "tile too small for 256 threads");
+  __shared__ __attribute__((aligned(16))) T As[2][BM * kRow];
+  __shared__ __attribute__((aligned(16))) T Ws[2][BN * kRow];
+
+  const int64_t M = a.n[0], N = a.n[1], K = a.n[2];
+  const int64_t lda = a.n[4], ldw = a.n[5], ldc = a.n[6];
+  const T* A = static_cast<const T*>(a.p[0]);
+  const T* W = static_cast<const T*>(a.p[1]);
+  T* C = static_cast<T*>(a.p[2]);
+
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t tiles = tiles_m * tiles_n;
+  const int64_t per_xcd = (tiles + 7) / 8;
+  const int64_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (tile >= tiles) return;  // whole block: no barrier is skipped by part of it
+  const int64_t m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fi = lane & 15, fg = lane >> 4;
+
+  // global -> register staging: vector v of a tile is row v / 8, k-chunk v % 8
+  uint4 ra[AV], rw[WV];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int t = 0; t < AV; ++t) {
+      const int v = tid + 256 * t, r = v >> 3, c = v & 7;
+      const int64_t m = m0 + r, k = k0 + c * 8;
+      ra[t] = (m < M && k < K) ? *reinterpret_cast<const uint4*>(A + m * lda + k) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < WV; ++t) {
+      const int v = tid + 256 * t, r = v >> 3, c = v & 7;
+      const int64_t n = n0 + r, k = k0 + c * 8;
+      rw[t] = (n < N && k < K) ? *reinterpret_cast<const uint4*>(W + n * ldw + k) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int t = 0; t < AV; ++t) {
+      const int v = tid + 256 * t, r = v >> 3, c = v & 7;
+      *reinterpret_cast<uint4*>(&As[buf][r * kRow + c * 8]) = ra[t];
+    }
+#pragma unroll
+    for (int t = 0; t < WV; ++t) {
+      const int v = tid + 256 * t, r = v >> 3, c = v & 7;
+      *reinterpret_cast<uint4*>(&Ws[buf][r * kRow + c * 8]) = rw[t];
+    }
+  };
+
+  f4v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < K; k0 += kBK) {
+    const bool more = k0 + kBK < K;
+    if (more) load_stage(k0 + kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      uint4 fa[TM], fw[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[i] = *reinterpret_cast<const uint4*>(&As[buf][(wm * (BM / 2) + i * 16 + fi) * kRow + ks * 32 + fg * 8]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fw[j] = *reinterpret_cast<const uint4*>(&Ws[buf][(wn * (BN / 2) + j * 16 + fi) * kRow + ks * 32 + fg * 8]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::step(fa[i], fw[j], acc[i][j]);
+    }
+    if (more) store_stage(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t n = n0 + wn * (BN / 2) + j * 16 + fi;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * (BM / 2) + i * 16 + fg * 4 + r;
+        if (m < M && n < N) C[m * ldc + n] = E::from_f(acc[i][j][r]);
+      }
+    }
+}
+
+template <typename T>
+const void* pick_gemm(bool big) {
+  return big ? reinterpret_cast<const void*>(&k_gemm_nt<T, 128, 128>)
+             : reinterpret_cast<const void*>(&k_gemm_nt<T, 64, 64>);
+}
+
+const char* plan_gemm(KArgs& a, Launch& l) {
+  const int64_t M = a.n[0], N = a.n[1], K = a.n[2];
+  const int dt = static_cast<int>(a.n[3]);
+  if (M <= 0 || N <= 0 || K <= 0) return "gemm: empty operands";
+  if (dt != F16 && dt != BF16) return "gemm: float16 or bfloat16 operands required";
+  if (K % 8 || a.n[4] % 8 || a.n[5] % 8) return "gemm: k and row strides must be multiples of 8 elements";
+  if (a.n[4] < K || a.n[5] < K || a.n[6] < N) return "gemm: row stride shorter than the row";
+  // 128 x 128 tiles once they fill the chip twice over, else 64 x 64
+  const int64_t big_tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  const bool big = big_tiles >= 512;
+  const int64_t bm = big ? 128 : 64;
+  const int64_t tiles = ((M + bm - 1) / bm) * ((N + bm - 1) / bm);
+  const int64_t blocks = 8 * ((tiles + 7) / 8);
+  if (blocks > 2147483647) return "gemm: too many tiles";
+  l.func = dt == F16 ? pick_gemm<__half>(big) : pick_gemm<bf16_t>(big);
+  l.grid = dim3(static_cast<unsigned>(blocks));
+  l.block = dim3(256);
+  l.shmem = 0;
+  return nullptr;
+}
+
+}  // namespace
+
+CHIP_REGISTER_KIND(CHIP_K_GEMM, plan_gemm);
+
+}  // namespace chip

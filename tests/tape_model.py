@@ -420,6 +420,15 @@ def s_gemv(mem, p, n, f):
     return 0
 
 
+def s_gemm(mem, p, n, f):
+    M, N, K, dt, lda, ldw, ldc = n[0:7]
+    A = load(mem, p[0], dt, np.arange(M)[:, None] * lda + np.arange(K)[None, :])
+    W = load(mem, p[1], dt, np.arange(N)[:, None] * ldw + np.arange(K)[None, :])
+    C = _round((A.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32), dt)
+    store(mem, p[2], dt, (np.arange(M)[:, None] * ldc + np.arange(N)[None, :]).reshape(-1), C.reshape(-1))
+    return 0
+
+
 def s_decode_attn(mem, p, n, f):
     B, H, KV, C, dt = n[0:5]
     qs, ks, vs = n[5:8], n[8:11], n[11:14]
@@ -478,5 +487,5 @@ STEP = {
     P.K_FILL: s_fill, P.K_COPY: s_copy, P.K_ELEMENTWISE: s_elementwise, P.K_REDUCE: s_reduce,
     P.K_GATHER: s_gather, P.K_MATMUL: s_matmul, P.K_SOFTMAX: s_softmax, P.K_RMSNORM: s_rmsnorm,
     P.K_ROPE: s_rope, P.K_SDPA: s_sdpa, P.K_KV_WRITE: s_kv_write, P.K_KV_PLACE: s_kv_place,
-    P.K_GEMV: s_gemv, P.K_DECODE_ATTN: s_decode_attn,
+    P.K_GEMV: s_gemv, P.K_GEMM: s_gemm, P.K_DECODE_ATTN: s_decode_attn,
 }

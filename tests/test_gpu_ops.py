@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from chomikgrad import Tensor, compile_graph, realize
-from chomikgrad.dtypes import BFLOAT16, bf16_to_float32, to_bf16
+from chomikgrad.dtypes import BFLOAT16, as_dtype, bf16_to_float32, dtype_name, to_bf16
 from chomikgrad.hip_backend import HIPArray
 
 pytestmark = pytest.mark.gpu
@@ -151,6 +151,30 @@ def test_gemv_linear_variants(hip, dtype, rows):
     tolerance = 1e-4 if dtype == np.float32 else 3e-2
     for g, e in zip(got, expected):
         np.testing.assert_allclose(as_float(g), as_float(e), rtol=tolerance, atol=tolerance)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("shape", [(37, 200, 72), (130, 96, 512), (9, 4100, 264), (2048, 4096, 256)],
+                         ids=["ragged", "tall", "wide", "large-tiles"])
+def test_gemm_linear_matches_fp32_reference(hip, dtype, shape):
+    """Linears with more than 8 rows run the MFMA GEMM (K_GEMM): fp32
+    accumulation of the 16-bit operands and one rounding, against a float32
+    matmul of the same rounded inputs.  Shapes cover ragged M/N/K edges, both
+    tile sizes, and K a multiple of 8 but not of the 64-column stage."""
+    M, N, K = shape
+    announce(f"gemm {dtype_name(dtype)} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    xh = as_dtype(rng.normal(size=(1, M, K)).astype(np.float32), dtype)
+    wh = as_dtype((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype)
+    x, w = Tensor(xh), Tensor(wh)
+    program = compile_graph(x @ w.T, compiler="hip")
+    assert "gemm" in program.source
+    (got,) = program()
+    xf = as_float(xh).reshape(M, K)
+    wf = as_float(wh)
+    expected = xf @ wf.T
+    tolerance = 1e-2 if dtype == np.float16 else 2e-2
+    np.testing.assert_allclose(as_float(got).reshape(M, N), expected, rtol=tolerance, atol=tolerance)
 
 
 def test_empty_tensors(hip):

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from chomikgrad import Tensor, realize, synthetic
-from chomikgrad._planner import K_DECODE_ATTN, K_GEMV, K_KV_PLACE, K_KV_WRITE, K_SDPA, plan_graph
+from chomikgrad._planner import K_DECODE_ATTN, K_GEMM, K_GEMV, K_KV_PLACE, K_KV_WRITE, K_SDPA, plan_graph
 from chomikgrad.dtypes import BFLOAT16, bf16_to_float32, to_bf16
 from chomikgrad.llama import (
     LlamaBatchedDecoderStep,
@@ -156,6 +156,31 @@ def test_prefill_with_cache_placement():
     _, got = model_run(outputs, [tokens])
     for value, reference in zip(got, expected):
         np.testing.assert_allclose(value, reference, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+def test_half_precision_prefill_uses_mfma_gemm(dtype):
+    """Prefill linears of a 16-bit model with more than 8 rows become K_GEMM
+    steps (row-major activations times W^T, fp32 accumulation, one rounding):
+    the tape model of those steps matches the oracle's np.matmul."""
+    config = LlamaConfig(vocab_size=128, hidden_size=256, intermediate_size=688, num_hidden_layers=1,
+                         num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64)
+    host = synthetic.host_weights(config, dtype, seed=11)
+    weights = synthetic.weights_as_tensors(host)
+    S = 12
+    model = LlamaForCausalLM(config, weights, sequence_length=S, cache_length=16, dtype=dtype)
+    ids = np.random.default_rng(4).integers(0, 128, (1, S)).astype(np.int32)
+    tokens = Tensor(ids, copy=False)
+    outputs = model.prefill(tokens, Tensor(position_selector(S - 1, S, dtype=dtype)))
+    expected = realize(*outputs, compiler="cpu")
+    planned, got = model_run(outputs, [tokens])
+    gemms = [s for s in planned.steps if s.kind == K_GEMM]
+    assert len(gemms) == 7  # q, k, v, o, gate, up, down
+    for value, reference in zip(got, expected):
+        v, r = np.asarray(value), np.asarray(reference)
+        if dtype is BFLOAT16:
+            v, r = bf16_to_float32(v), bf16_to_float32(r)
+        np.testing.assert_allclose(v.astype(np.float32), r.astype(np.float32), rtol=1e-2, atol=2e-2)
 
 
 def test_block_verify_uses_kv_place():

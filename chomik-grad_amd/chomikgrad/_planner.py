@@ -670,8 +670,33 @@ class Emitter:
         q, k, v, mask = args
         out = self.new_value(node.shape, node.dtype, "sdpa")
         if out.size:
-            self.add(K_SDPA, [q, k, v, mask], [out], divisor=float(1.0 / float(scale)))
+            causal = self._causal_mask_value(mask, q.shape[2], k.shape[2], q.dtype)
+            self.add(K_SDPA, [q, k, v, mask], [out], divisor=float(1.0 / float(scale)),
+                     causal=causal)
         return out
+
+    @staticmethod
+    def _causal_mask_value(mask: Optional[PV], T: int, C: int, dtype) -> Optional[float]:
+        """The value above the diagonal if ``mask`` is a captured constant
+        holding exactly the causal triangle (0 on and below the diagonal, one
+        value <= -1e4 above it) for T == C, else None."""
+        if mask is None or T != C or T < 2 or mask.storage.kind != "const":
+            return None
+        leaf = getattr(mask.storage, "leaf", None)
+        if leaf is None or leaf.value is None or mask.offset or np.dtype(mask.dtype) != np.dtype(dtype):
+            return None
+        value = np.asarray(leaf.value)
+        if value.size != T * C:
+            return None
+        grid = value.reshape(T, C)
+        if grid.dtype == BFLOAT16:
+            from .dtypes import bf16_to_float32
+            grid = bf16_to_float32(grid)
+        grid = grid.astype(np.float32)
+        above = grid[np.triu_indices(T, 1)]
+        if not np.all(np.tril(grid) == 0) or above.size == 0 or not np.all(above == above[0]):
+            return None
+        return float(above[0]) if above[0] <= -1e4 + 16 else None
 
     def lower_softmax(self, node, args, axis):
         source = args[0]
@@ -1085,7 +1110,11 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         mask_strides = broadcast_strides(mask, (b, h, t, c))
         ints = [b, h, t, c, hd, k.shape[1], dtype_code(q.dtype)]
         ints += list(q.strides) + list(k.strides) + list(v.strides) + mask_strides + [dtype_code(mask.dtype)]
-        return kind, [_ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(out)], ints, [a["divisor"]]
+        causal = a.get("causal")
+        aligned = all(pv.offset % 8 == 0 for pv in (q, k, v))
+        ints += [1 if causal is not None else 0, 1 if aligned else 0]
+        return kind, [_ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(out)], ints, [
+            a["divisor"], causal if causal is not None else 0.0]
     if kind == K_KV_WRITE:
         cache, x, w = step.ins
         out = step.outs[0]

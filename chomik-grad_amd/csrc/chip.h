@@ -208,6 +208,10 @@ using Planner = const char* (*)(KArgs& a, Launch& l);
 void register_kind(int kind, Planner planner);
 Planner planner_for(int kind);
 
+// MFMA prefill attention (k_flash.hip): fills ``l`` and returns true when a
+// K_SDPA step fits it.
+bool plan_flash_prefill(KArgs& a, Launch& l);
+
 // The library's device error word (device pointer), defined in runtime.hip.
 int* device_error_word();
 // Record an error message for chip_last_error(); returns ``code``.

@@ -167,6 +167,7 @@ const char* plan_sdpa(KArgs& a, Launch& l) {
   for (int i = 0; i < 6; ++i)
     if (a.n[i] <= 0) return "sdpa: empty dimension";
   if (a.n[1] % a.n[5]) return "sdpa: heads not divisible by KV heads";
+  if (plan_flash_prefill(a, l)) return nullptr;
   if (a.n[4] > 256) return "sdpa: head size above 256";
   if (a.n[3] > 32768) return "sdpa: more than 32768 keys for the generic kernel";
   const int64_t rows = a.n[0] * a.n[1] * a.n[2];

@@ -177,6 +177,51 @@ def test_gemm_linear_matches_fp32_reference(hip, dtype, shape):
     np.testing.assert_allclose(as_float(got).reshape(M, N), expected, rtol=tolerance, atol=tolerance)
 
 
+def _sdpa_graph(q, k, v, mask, heads, dtype):
+    """The llama builder's portable GQA attention, tagged ``sdpa``."""
+    kv = k.shape[1]
+    ones = Tensor(np.ones((1, 1, heads // kv, 1, 1), np.float32), dtype=dtype)
+
+    def repeat(x):
+        b, _, t, hd = x.shape
+        return (x.reshape(b, kv, 1, t, hd) * ones).reshape(b, heads, t, hd)
+
+    scores = (q @ repeat(k).transpose(-2, -1)) / np.sqrt(64) + mask
+    out = scores.softmax(axis=-1) @ repeat(v)
+    out._node.lowering = ("sdpa", (q._node, k._node, v._node, mask._node), 1 / np.sqrt(64))
+    return out
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("T,mask_kind", [(100, "causal"), (300, "causal"), (70, "dense")])
+def test_prefill_attention_matches_oracle(hip, dtype, T, mask_kind):
+    """Prefill attention (K_SDPA with 16+ query rows, head size 64) runs the
+    MFMA kernel: a captured causal triangle is proved and applied
+    arithmetically (tiles above the diagonal skipped); any other mask is read
+    from memory.  Ragged T covers partial query and key tiles; 8 query heads
+    over 2 KV heads covers GQA."""
+    announce(f"prefill attention {dtype_name(dtype)} T={T} {mask_kind}")
+    rng = np.random.default_rng(T)
+    H, KV = 8, 2
+    q = Tensor(as_dtype(rng.normal(size=(1, H, T, 64)).astype(np.float32), dtype), copy=False)
+    k = Tensor(as_dtype(rng.normal(size=(1, KV, T, 64)).astype(np.float32), dtype), copy=False)
+    v = Tensor(as_dtype(rng.normal(size=(1, KV, T, 64)).astype(np.float32), dtype), copy=False)
+    if mask_kind == "causal":
+        host_mask = np.triu(np.full((T, T), -1e4, np.float32), k=1)
+    else:
+        host_mask = rng.uniform(-4.0, 0.0, size=(T, T)).astype(np.float32)
+    mask = Tensor(as_dtype(host_mask.reshape(1, 1, T, T), dtype))
+    out = _sdpa_graph(q, k, v, mask, H, dtype)
+    program = compile_graph(out, compiler="hip", dynamic_inputs=(q, k, v))
+    sdpa_steps = [s for s in program._planned.steps if s.attrs.get("divisor") is not None]
+    assert len(sdpa_steps) == 1
+    assert (sdpa_steps[0].attrs["causal"] is not None) == (mask_kind == "causal")
+    (got,) = program()
+    (expected,) = realize(out, compiler="cpu")
+    tolerance = 1e-2 if dtype == np.float16 else 3e-2
+    np.testing.assert_allclose(as_float(got), as_float(expected), rtol=tolerance, atol=tolerance)
+
+
 def test_empty_tensors(hip):
     announce("empty tensors")
     empty = Tensor(np.empty((0, 4), dtype=np.float32))

@@ -95,6 +95,57 @@ def weights_bytes(config, itemsize: int) -> int:
     return total
 
 
+MFMA_PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 matrix peak
+
+
+def prefill_flops(config, tokens: int) -> float:
+    """Algorithmic FLOPs of one causal prefill: every linear over all rows,
+    q.k and p.v over the causal triangle, the lm_head for the selected row."""
+    from chomikgrad.llama import required_weight_shapes
+
+    shapes = required_weight_shapes(config)
+    linear = sum(int(np.prod(shape)) for name, shape in shapes.items()
+                 if name.endswith("proj.weight"))
+    attention = (4 * config.num_attention_heads * config.head_size * tokens * (tokens + 1) // 2
+                 * config.num_hidden_layers)
+    lm_head = 2 * config.hidden_size * config.vocab_size
+    return 2.0 * tokens * linear + attention + lm_head
+
+
+def prefill_measurement(runtime, config, device, lib, tokens: int, runs: int) -> dict:
+    """C3: one prompt of ``tokens`` ids through the prefill program (compiled
+    and warmed first), timed with HIP events on the library stream."""
+    from chomikgrad import synthetic
+
+    prompt = synthetic.prompt_ids(config.vocab_size, tokens, seed=0)
+    runtime.prefill(prompt, tokens)
+    device.synchronize()
+    start, stop = ctypes.c_void_p(), ctypes.c_void_p()
+    lib.call("chip_event_create", ctypes.byref(start))
+    lib.call("chip_event_create", ctypes.byref(stop))
+    samples = []
+    for _ in range(runs):
+        lib.call("chip_event_record", start)
+        runtime.prefill(prompt, tokens)
+        lib.call("chip_event_record", stop)
+        device.synchronize()
+        ms = ctypes.c_float(0.0)
+        lib.call("chip_event_elapsed_ms", start, stop, ctypes.byref(ms))
+        samples.append(ms.value)
+    lib.call("chip_event_destroy", start)
+    lib.call("chip_event_destroy", stop)
+    best = min(samples)
+    flops = prefill_flops(config, tokens)
+    tflops = flops / (best * 1e-3) / 1e12
+    return {
+        "workload": f"C3: TinyLlama-1.1B-shape fp16 causal prefill of {tokens} tokens",
+        "tokens": tokens, "ms": round(best, 3), "ms_runs": [round(v, 3) for v in samples],
+        "tok_per_s": round(tokens / (best * 1e-3), 1),
+        "algorithmic_tflop": round(flops / 1e12, 4), "achieved_tflops": round(tflops, 1),
+        "peak_tflops": MFMA_PEAK_FP16_TFLOPS, "mfma_utilisation": round(tflops / MFMA_PEAK_FP16_TFLOPS, 4),
+    }
+
+
 def cpu_baseline(config, weights, dtype, context: int, first_position: int, steps: int) -> dict:
     """Oracle decode steps on the host: the reference's NumPy cpu-plugin
     algorithm, float16, with zero-filled caches of the real context length.
@@ -146,6 +197,8 @@ def main() -> int:
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="only copy a MIB-sized device buffer three times (counter calibration) and exit")
     parser.add_argument("--cpu-steps", type=int, default=3, help="oracle decode steps for the CPU baseline")
+    parser.add_argument("--prefill-tokens", type=int, default=2048, help="C3 prefill length (0 skips it)")
+    parser.add_argument("--prefill-runs", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -277,6 +330,12 @@ def main() -> int:
     bytes_per_token = float(np.mean(weights_bytes(config, 2) + kv_bytes * (positions + 1) + kv_bytes))
     step_gbps = bytes_per_token * decode_tps / 1e9
 
+    prefill_c3 = None
+    if args.prefill_tokens:
+        log(f"C3 prefill of {args.prefill_tokens} tokens")
+        prefill_c3 = prefill_measurement(runtime, config, device, lib, args.prefill_tokens, args.prefill_runs)
+        log(f"C3 prefill: {prefill_c3['ms']} ms, {prefill_c3['achieved_tflops']} TFLOP/s")
+
     baseline = None
     if not args.no_cpu_baseline:
         log("timing the NumPy oracle on the host (bounded sample)")
@@ -311,6 +370,7 @@ def main() -> int:
                           "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
         "gpu_event_ms_per_step": round(gpu_ms.value / args.steps, 4),
         "prefill_tok_per_s": round(PROMPT / prefill_seconds, 1),
+        "prefill_c3": prefill_c3,
         "kernel_breakdown": breakdown,
         "first_tokens": tokens[:16],
     }

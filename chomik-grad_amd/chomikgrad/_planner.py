@@ -555,7 +555,41 @@ class Emitter:
         return out
 
     def op_matmul(self, node, args):
-        return self.matmul(node, args[0], args[1])
+        a, b = args
+        if self._is_placement(a, b, node):
+            # A @ eye(S, C): A's columns in the first S output columns, zeros
+            # after them (the prefill KV-cache placement, llama.py
+            # LlamaForCausalLM.prefill)
+            out = self.new_value(node.shape, node.dtype, "placement")
+            self.add(K_FILL, [], [out], words=(out.size * out.itemsize + 3) // 4)
+            view = PV(a.shape, node.dtype, out.strides[:-1] + (1,), out.storage, out.offset)
+            self.add(K_COPY, [a], [view])
+            return out
+        return self.matmul(node, a, b)
+
+    @staticmethod
+    def _is_placement(a: PV, b: PV, node) -> bool:
+        """b is a captured constant equal to eye(S, C), S <= C, and the
+        product keeps A's dtype: then A @ b copies A into the first S
+        columns.  (Only for finite A does this equal the float product: an
+        inf in A would have spread NaN through its row.)"""
+        if len(b.shape) != 2 or b.storage.kind != "const" or b.offset or not b.contiguous():
+            return False
+        if not (a.dtype == b.dtype == node.dtype) or len(a.shape) < 2 or len(node.shape) != len(a.shape):
+            return False
+        S, C = b.shape
+        if a.shape[-1] != S or S > C or tuple(node.shape[:-1]) != tuple(a.shape[:-1]):
+            return False
+        leaf = getattr(b.storage, "leaf", None)
+        if leaf is None or leaf.value is None:
+            return False
+        value = np.asarray(leaf.value)
+        if value.shape != (S, C):
+            return False
+        if value.dtype == BFLOAT16:
+            from .dtypes import bf16_to_float32
+            value = bf16_to_float32(value)
+        return bool(np.array_equal(value.astype(np.float32), np.eye(S, C, dtype=np.float32)))
 
     def matmul(self, node, a: PV, b: PV) -> PV:
         out = self.new_value(node.shape, node.dtype, "matmul")
@@ -1040,8 +1074,10 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         return kind, [_ptr(out)], [a["words"], 0], []
     if kind == K_COPY:
         src, dst = step.ins[0], step.outs[0]
+        strided = not dst.contiguous()
         return kind, [_ptr(src), _ptr(dst)], (
             [src.size, len(src.shape)] + _pad(src.shape, 8, 1) + _pad(src.strides, 8) + [src.itemsize]
+            + [1 if strided else 0] + _pad(dst.strides if strided else (), 8)
         ), []
     if kind == K_ELEMENTWISE:
         out = step.outs[0]

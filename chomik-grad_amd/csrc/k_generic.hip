@@ -43,21 +43,25 @@ const char* plan_fill(KArgs& a, Launch& l) {
 // ---------------------------------------------------------------- copy
 // Materialise a strided view contiguously (raw bits, any element size).
 // p[0] src, p[1] dst; n[0] N, n[1] ndim, n[2..9] sizes, n[10..17] src
-// strides (elements), n[18] element bytes (1, 2, 4, 8).
+// strides (elements), n[18] element bytes (1, 2, 4, 8), n[19] dst is strided
+// (else contiguous), n[20..27] dst strides (elements).
 template <typename W>
 __global__ void k_copy_strided(KArgs a) {
   const W* src = static_cast<const W*>(a.p[0]);
   W* dst = static_cast<W*>(a.p[1]);
   const int nd = static_cast<int>(a.n[1]);
+  const bool strided_dst = a.n[19] != 0;
   for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < a.n[0];
        i += int64_t(gridDim.x) * blockDim.x) {
-    int64_t rem = i, off = 0;
+    int64_t rem = i, off = 0, doff = 0;
     for (int d = nd - 1; d >= 0; --d) {
       const int64_t size = a.n[2 + d];
-      off += (rem % size) * a.n[10 + d];
+      const int64_t c = rem % size;
+      off += c * a.n[10 + d];
+      doff += c * a.n[20 + d];
       rem /= size;
     }
-    dst[i] = src[off];
+    dst[strided_dst ? doff : i] = src[off];
   }
 }
 

@@ -301,48 +301,70 @@ const char* plan_kv_place(KArgs& a, Launch& l) {
 
 // ---------------------------------------------------------------- argmax
 // First index of the maximum; NaN counts as the maximum (NumPy argmax).
-struct Best {
-  float v;
-  int64_t i;
-};
-__device__ __forceinline__ Best better(Best x, Best y) {
-  const bool xn = x.v != x.v, yn = y.v != y.v;
-  if (xn || yn) {
-    if (xn && yn) return x.i <= y.i ? x : y;
-    return xn ? x : y;
+// Each row is split over up to kArgBlocks blocks.  Every element becomes a
+// 64-bit key -- order-preserving float bits (NaN above everything, -0 folded
+// into +0) over the inverted index -- so the largest key is the first
+// maximum.  Blocks fold their best key into the row's word with atomicMax;
+// a self-resetting ticket elects the last block, which reads the result and
+// clears the word and the ticket for the next launch.
+constexpr int kArgBlocks = 64;
+
+__device__ __forceinline__ uint64_t arg_key(float v, int64_t j) {
+  uint32_t ord;
+  if (v != v) {
+    ord = 0xffffffffu;
+  } else {
+    if (v == 0.f) v = 0.f;
+    const uint32_t bits = __float_as_uint(v);
+    ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
   }
-  if (x.v > y.v) return x;
-  if (y.v > x.v) return y;
-  return x.i <= y.i ? x : y;
+  return (static_cast<uint64_t>(ord) << 32) | (0xffffffffu - static_cast<uint32_t>(j));
 }
 
-__device__ Best row_argmax(const void* src, int dt, int64_t row, int64_t cols) {
-  __shared__ float sv[16];
-  __shared__ int64_t si[16];
-  Best best{-INFINITY, cols};
-  for (int64_t j = threadIdx.x; j < cols; j += blockDim.x)
-    best = better(best, Best{load_f(src, row * cols + j, dt), j});
-  if (best.i == cols) best.i = INT64_MAX;  // no element seen by this thread
+__device__ __forceinline__ int64_t key_index(uint64_t key) {
+  return static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(key & 0xffffffffu));
+}
+
+// Row blockIdx.y, slice blockIdx.x of gridDim.x.  Returns true in every
+// thread of the row's last block; its thread 0 then holds the row's key.
+__device__ bool argmax_slices(const void* src, int dt, int64_t cols, uint64_t* keys, int* tickets,
+                              uint64_t* final_key) {
+  __shared__ uint64_t sk[4];
+  __shared__ int last;
+  const int64_t row = blockIdx.y;
+  const int64_t chunk = (cols + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = blockIdx.x * chunk, hi = lo + chunk < cols ? lo + chunk : cols;
+  uint64_t key = 0;
+  for (int64_t j = lo + threadIdx.x; j < hi; j += blockDim.x) {
+    const uint64_t k = arg_key(load_f(src, row * cols + j, dt), j);
+    key = k > key ? k : key;
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    Best other{__shfl_xor(best.v, o, 64), __shfl_xor(best.i, o, 64)};
-    best = better(best, other);
+    const uint64_t other = __shfl_xor(key, o, 64);
+    key = other > key ? other : key;
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) sk[wave] = key;
   __syncthreads();
-  if (lane == 0) {
-    sv[wave] = best.v;
-    si[wave] = best.i;
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) key = sk[w] > key ? sk[w] : key;
+    atomicMax(reinterpret_cast<unsigned long long*>(&keys[row]), static_cast<unsigned long long>(key));
+    __threadfence();
+    last = atomicAdd(&tickets[row], 1) == static_cast<int>(gridDim.x) - 1;
+    if (last) {
+      *final_key = atomicExch(reinterpret_cast<unsigned long long*>(&keys[row]), 0ull);
+      atomicExch(&tickets[row], 0);
+    }
   }
   __syncthreads();
-  Best total{sv[0], si[0]};
-  for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) total = better(total, Best{sv[w], si[w]});
-  return total;
+  return last;
 }
 
-__global__ __launch_bounds__(1024) void k_argmax(const void* src, int dt, int64_t cols, int64_t* out) {
-  const Best best = row_argmax(src, dt, blockIdx.x, cols);
-  if (threadIdx.x == 0) out[blockIdx.x] = best.i;
+__global__ __launch_bounds__(256) void k_argmax(const void* src, int dt, int64_t cols, int64_t* out,
+                                                uint64_t* keys, int* tickets) {
+  uint64_t key = 0;
+  if (argmax_slices(src, dt, cols, keys, tickets, &key) && threadIdx.x == 0) out[blockIdx.y] = key_index(key);
 }
 
 struct Advance {
@@ -361,13 +383,15 @@ struct Advance {
   int64_t cache_length;
   int64_t rows;
   int* error;
+  uint64_t* keys;
+  int* tickets;
 };
 
-__global__ __launch_bounds__(1024) void k_greedy_advance(Advance a) {
-  const int64_t row = blockIdx.x;
-  const Best best = row_argmax(a.logits, a.logits_dtype, row, a.cols);
-  if (threadIdx.x != 0) return;
-  const int32_t token = static_cast<int32_t>(best.i);
+__global__ __launch_bounds__(256) void k_greedy_advance(Advance a) {
+  uint64_t key = 0;
+  if (!argmax_slices(a.logits, a.logits_dtype, a.cols, a.keys, a.tickets, &key) || threadIdx.x != 0) return;
+  const int64_t row = blockIdx.y;
+  const int32_t token = static_cast<int32_t>(key_index(key));
   a.tokens[row] = token;
   if (a.history) a.history[a.step * a.rows + row] = token;
   if (!a.position) return;
@@ -384,14 +408,49 @@ __global__ __launch_bounds__(1024) void k_greedy_advance(Advance a) {
   }
 }
 
+// Per-row key words and tickets (zeroed once; the kernels leave them zero).
+uint64_t* g_arg_keys = nullptr;
+int* g_arg_tickets = nullptr;
+int64_t g_arg_rows = 0;
+
+int arg_scratch(int64_t rows, hipStream_t stream) {
+  if (rows <= g_arg_rows) return CHIP_OK;
+  const int64_t cap = rows < 64 ? 64 : rows;
+  if (g_arg_keys) {
+    if (hipStreamSynchronize(stream) != hipSuccess) return set_error(CHIP_EHIP, "argmax: stream failed");
+    (void)hipFree(g_arg_keys);
+    (void)hipFree(g_arg_tickets);
+    g_arg_keys = nullptr;
+    g_arg_tickets = nullptr;
+    g_arg_rows = 0;
+  }
+  if (hipMalloc(reinterpret_cast<void**>(&g_arg_keys), cap * sizeof(uint64_t)) != hipSuccess ||
+      hipMalloc(reinterpret_cast<void**>(&g_arg_tickets), cap * sizeof(int)) != hipSuccess)
+    return set_error(CHIP_ENOMEM, "argmax: cannot allocate row words");
+  if (hipMemset(g_arg_keys, 0, cap * sizeof(uint64_t)) != hipSuccess ||
+      hipMemset(g_arg_tickets, 0, cap * sizeof(int)) != hipSuccess)
+    return set_error(CHIP_EHIP, "argmax: cannot clear row words");
+  g_arg_rows = cap;
+  return CHIP_OK;
+}
+
+dim3 arg_grid(int64_t rows, int64_t cols) {
+  int64_t blocks = (cols + 255) / 256;
+  if (blocks > kArgBlocks) blocks = kArgBlocks;
+  if (blocks < 1) blocks = 1;
+  return dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(rows));
+}
+
 }  // namespace
 
 int launch_argmax(const void* src, int dtype, int64_t rows, int64_t cols, int64_t* out_dev,
                   hipStream_t stream) {
   if (dtype != F32 && dtype != F16 && dtype != BF16) return set_error(CHIP_EINVAL, "argmax: float dtype required");
-  if (rows > 2147483647) return set_error(CHIP_EINVAL, "argmax: too many rows");
-  hipLaunchKernelGGL(k_argmax, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, stream, src, dtype,
-                     cols, out_dev);
+  if (rows > 65535 || cols > 0xffffffffLL) return set_error(CHIP_EINVAL, "argmax: too many rows or columns");
+  int rc = arg_scratch(rows, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_argmax, arg_grid(rows, cols), dim3(256), 0, stream, src, dtype, cols, out_dev,
+                     g_arg_keys, g_arg_tickets);
   if (hipGetLastError() != hipSuccess) return set_error(CHIP_EHIP, "argmax launch failed");
   return CHIP_OK;
 }
@@ -405,11 +464,14 @@ int launch_greedy_advance(const void* logits, int logits_dtype, int64_t rows, in
     return set_error(CHIP_EINVAL, "greedy advance: float logits required");
   if ((attention_mask || write_mask) && mask_dtype != F32 && mask_dtype != F16 && mask_dtype != BF16)
     return set_error(CHIP_EINVAL, "greedy advance: float masks required");
+  if (rows > 65535 || cols > 0xffffffffLL) return set_error(CHIP_EINVAL, "greedy advance: too many rows or columns");
+  int rc = arg_scratch(rows, stream);
+  if (rc) return rc;
   Advance a{logits, logits_dtype, mask_dtype, cols, static_cast<int32_t*>(tokens_out),
             static_cast<int32_t*>(history), step, static_cast<int32_t*>(position),
             attention_mask, mask_row, write_mask, write_row, cache_length, rows,
-            device_error_word()};
-  hipLaunchKernelGGL(k_greedy_advance, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, stream, a);
+            device_error_word(), g_arg_keys, g_arg_tickets};
+  hipLaunchKernelGGL(k_greedy_advance, arg_grid(rows, cols), dim3(256), 0, stream, a);
   if (hipGetLastError() != hipSuccess) return set_error(CHIP_EHIP, "greedy advance launch failed");
   return CHIP_OK;
 }

@@ -192,12 +192,13 @@ def s_copy(mem, p, n, f):
     count, nd = n[0], n[1]
     size = n[18]
     index = strided_index(n[2:2 + nd], n[10:10 + nd])
+    target = strided_index(n[2:2 + nd], n[20:20 + nd]) if n[19] else np.arange(count)
     if size == 1:
         src = mem.slots[p[0][0]][p[0][1]:]
-        mem.slots[p[1][0]][p[1][1]:p[1][1] + count] = src[index]
+        mem.slots[p[1][0]][p[1][1] + target] = src[index]
         return 0
     code = {2: 2, 4: 3, 8: 4}[size]
-    mem.flat(p[1], code)[:count] = mem.flat(p[0], code)[index]
+    mem.flat(p[1], code)[target] = mem.flat(p[0], code)[index]
     return 0
 
 

@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 
 from chomikgrad import Tensor, realize, synthetic
-from chomikgrad._planner import K_DECODE_ATTN, K_GEMM, K_GEMV, K_KV_PLACE, K_KV_WRITE, K_SDPA, plan_graph
+from chomikgrad._planner import (K_DECODE_ATTN, K_FILL, K_GEMM, K_GEMV, K_KV_PLACE, K_KV_WRITE, K_MATMUL,
+                                 K_SDPA, plan_graph)
 from chomikgrad.dtypes import BFLOAT16, bf16_to_float32, to_bf16
 from chomikgrad.llama import (
     LlamaBatchedDecoderStep,
@@ -176,6 +177,10 @@ def test_half_precision_prefill_uses_mfma_gemm(dtype):
     planned, got = model_run(outputs, [tokens])
     gemms = [s for s in planned.steps if s.kind == K_GEMM]
     assert len(gemms) == 7  # q, k, v, o, gate, up, down
+    # the cache placements K^T @ eye(S, C) become fill + strided copy; the one
+    # generic matmul left is the last-row selector
+    assert sum(s.kind == K_FILL for s in planned.steps) == 2
+    assert sum(s.kind == K_MATMUL for s in planned.steps) == 1
     for value, reference in zip(got, expected):
         v, r = np.asarray(value), np.asarray(reference)
         if dtype is BFLOAT16:

@@ -112,6 +112,55 @@ def prefill_flops(config, tokens: int) -> float:
     return 2.0 * tokens * linear + attention + lm_head
 
 
+def step_flops(step) -> int:
+    """Algorithmic FLOPs of a prefill matrix kernel (0 for the others):
+    2 M N K for a GEMM; q.k and p.v over the visited keys for attention
+    (the causal triangle when the mask was proved causal)."""
+    from chomikgrad._planner import K_GEMM, K_SDPA
+
+    if step.kind == K_GEMM:
+        return 2 * step.attrs["rows"] * step.attrs["N"] * step.attrs["K"]
+    if step.kind == K_SDPA:
+        b, h, t, hd = step.ins[0].shape
+        c = step.ins[1].shape[2]
+        keys = t * (t + 1) // 2 if step.attrs.get("causal") is not None else t * c
+        return 4 * b * h * hd * keys
+    return 0
+
+
+def plan_label(step) -> str:
+    """Kernel kind plus, for GEMMs, M x N x K."""
+    from chomikgrad._planner import K_GEMM, KIND_NAMES
+
+    if step.kind == K_GEMM:
+        return f"gemm {step.attrs['rows']}x{step.attrs['N']}x{step.attrs['K']}"
+    return kernel_label(step)
+
+
+def plan_breakdown(program, lib, *, rounds: int, flops=None) -> dict:
+    """Average duration of each kernel group of a plan: every instance of a
+    label launched round-robin ``rounds`` times between one HIP event pair
+    on the library stream (chip_plan_time_repeat)."""
+    steps = program._planned.steps
+    groups = {}
+    for index, step in enumerate(steps):
+        groups.setdefault(plan_label(step), []).append(index)
+    out = {}
+    for label, indices in groups.items():
+        ids = (ctypes.c_int64 * len(indices))(*indices)
+        ms = ctypes.c_float(0.0)
+        lib.call("chip_plan_time_repeat", program._plan, ids, ctypes.c_int64(len(indices)),
+                 ctypes.c_int64(rounds), ctypes.byref(ms))
+        entry = {"launches": len(indices), "avg_us": round(1e3 * ms.value, 2),
+                 "total_ms": round(ms.value * len(indices), 3)}
+        if flops is not None:
+            f = statistics.mean(flops(steps[i]) for i in indices)
+            if f:
+                entry["tflops"] = round(f / (ms.value * 1e-3) / 1e12, 1)
+        out[label] = entry
+    return out
+
+
 def prefill_measurement(runtime, config, device, lib, tokens: int, runs: int) -> dict:
     """C3: one prompt of ``tokens`` ids through the prefill program (compiled
     and warmed first), timed with HIP events on the library stream."""
@@ -137,12 +186,15 @@ def prefill_measurement(runtime, config, device, lib, tokens: int, runs: int) ->
     best = min(samples)
     flops = prefill_flops(config, tokens)
     tflops = flops / (best * 1e-3) / 1e12
+    program = runtime._prefill_programs[(tokens, tokens)][0]
+    breakdown = plan_breakdown(program, lib, rounds=2, flops=step_flops)
     return {
         "workload": f"C3: TinyLlama-1.1B-shape fp16 causal prefill of {tokens} tokens",
         "tokens": tokens, "ms": round(best, 3), "ms_runs": [round(v, 3) for v in samples],
         "tok_per_s": round(tokens / (best * 1e-3), 1),
         "algorithmic_tflop": round(flops / 1e12, 4), "achieved_tflops": round(tflops, 1),
         "peak_tflops": MFMA_PEAK_FP16_TFLOPS, "mfma_utilisation": round(tflops / MFMA_PEAK_FP16_TFLOPS, 4),
+        "kernel_breakdown": breakdown,
     }
 
 

@@ -29,6 +29,11 @@ FLAGS = [
     "-fPIC",
     # Packed fp32 instructions have given silent wrong results on these boxes.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Every rounding point written in the kernels is kept: no implicit fusion
+    # of a rounded product into the next add (fp16 round(a*b) + c would become
+    # v_fma_f16 and drop the product's rounding).  Kernels call fmaf where a
+    # fused multiply-add is meant.
+    "-ffp-contract=off",
     f"-I{REPO / 'include'}",
     f"-I{CSRC}",
     "-Wall",

@@ -57,6 +57,10 @@ GEMV_STAGE_BYTES = 48 * 1024
 # Waves sharing one GEMV row group (K split): 0 lets the kernel choose from
 # the row count; CHOMIK_HIP_GEMV_SPLIT=1/2/4 forces one (for tuning sweeps).
 GEMV_SPLIT = int(os.environ.get("CHOMIK_HIP_GEMV_SPLIT", "0"))
+# Decode attention: cache rows per workgroup = (32 for 2-byte, 16 for 4-byte
+# dtypes) x passes; 0 picks the passes from the shape, 1/2/4 forces them.
+DECODE_ATTN_PASSES = int(os.environ.get("CHOMIK_HIP_ATTN_PASSES", "0"))
+DECODE_ATTN_MAX_CHUNKS = 64
 SDPA_MAX_KEYS = 32768
 ARENA_ALIGN = 256
 SUPPORTED_TAGS = frozenset({"rms_norm", "rope", "sdpa", "softmax"})
@@ -908,6 +912,32 @@ def fuse_residual(steps: List[Step], outputs: List[PV]) -> List[Step]:
     return [s for s in steps if id(s) not in removed]
 
 
+def decode_attention_rows(itemsize: int) -> int:
+    """Cache rows one pass of the decode-attention workgroup covers: 256
+    threads, one 16-byte vector per lane, 64-element rows."""
+    return 256 // (64 * itemsize // 16)
+
+
+def decode_attention_passes(B: int, KV: int, C: int, itemsize: int) -> int:
+    """Passes (rows per workgroup / rows per pass) for the split-context
+    decode attention: the most rows per workgroup that still leaves >= 1024
+    workgroups, else one pass (short caches: as many workgroups as rows
+    allow, so the per-workgroup latency chain stays short)."""
+    rows = decode_attention_rows(itemsize)
+    if DECODE_ATTN_PASSES:
+        chosen = DECODE_ATTN_PASSES
+    else:
+        chosen = 1
+        for passes in (4, 2):
+            if B * KV * -(-C // (rows * passes)) >= 1024:
+                chosen = passes
+                break
+    # the combining workgroup merges at most 64 chunks per KV head
+    while chosen < 4 and -(-C // (rows * chosen)) > DECODE_ATTN_MAX_CHUNKS:
+        chosen *= 2
+    return chosen
+
+
 def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitter") -> List[Step]:
     """rope(q), rope(k), kv_write(K), kv_write(V), sdpa -> one decode_attention
     step (single new token, head size 64)."""
@@ -915,6 +945,7 @@ def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitte
     producer = _producer(steps)
     removed = set()
     tickets: Optional[PV] = None
+    partials: Dict[int, PV] = {}
     for index, step in enumerate(steps):
         if step.kind != K_SDPA:
             continue
@@ -953,15 +984,23 @@ def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitte
             continue
         if cache_k.strides[2:] != (64, 1) or cache_v.strides[2:] != (64, 1):
             continue
-        if C * 4 > 96 * 1024 or w.dtype != q.dtype or mask.dtype != q.dtype:
+        if w.dtype != q.dtype or mask.dtype != q.dtype or H // KV not in (1, 2, 4, 8):
             continue
         if tickets is None or tickets.size < B * KV:
             tickets = emitter.zeros(4 * max(B * KV, 64), "tickets")
+        passes = decode_attention_passes(B, KV, C, q.itemsize)
+        chunks = -(-C // (decode_attention_rows(q.itemsize) * passes))
+        if chunks > DECODE_ATTN_MAX_CHUNKS:
+            continue
+        floats = B * H * chunks * 66 if chunks > 1 else 1
+        if floats not in partials:
+            partials[floats] = emitter.zeros(4 * floats, "attention_partials")
         fused = Step(K_DECODE_ATTN,
-                     [rq.ins[0], rk.ins[0], xv, rq.ins[1], rq.ins[2], cache_k, cache_v, w, mask, tickets],
+                     [rq.ins[0], rk.ins[0], xv, rq.ins[1], rq.ins[2], cache_k, cache_v, w, mask, tickets,
+                      partials[floats]],
                      [step.outs[0], wk.outs[0], wv.outs[0]],
                      {"in_place": wk.attrs["in_place"], "table_length": rq.attrs["table_length"],
-                      "mode": rq.attrs["mode"], "divisor": step.attrs["divisor"]})
+                      "mode": rq.attrs["mode"], "divisor": step.attrs["divisor"], "passes": passes})
         steps[index] = fused
         removed.update({id(rq), id(rk), id(wk), id(wv)})
     return [s for s in steps if id(s) not in removed]
@@ -1172,7 +1211,7 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         ints += [dtype_code(placement.dtype), dtype_code(w.dtype)]
         return kind, [_ptr(cache), _ptr(x), _ptr(placement), _ptr(w), _ptr(out)], ints, []
     if kind == K_DECODE_ATTN:
-        q, k, v, position, table, cache_k, cache_v, w, mask, tickets = step.ins
+        q, k, v, position, table, cache_k, cache_v, w, mask, tickets, partials = step.ins
         out, out_k, out_v = step.outs
         B, H = q.shape[0], q.shape[1]
         KV, C = cache_k.shape[1], cache_k.shape[2]
@@ -1184,8 +1223,9 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
                 v.strides[0], v.strides[1], v.strides[3],
                 a["mode"], a["table_length"]] + list(cache_k.strides)
         ints += [ws[0], ws[2], ms[0], ms[1], ms[3], dtype_code(mask.dtype), dtype_code(w.dtype),
-                 1 if a["in_place"] else 0]
-        ptrs = [_ptr(pv) for pv in (q, k, v, position, table, cache_k, cache_v, w, mask, out, out_k, out_v, tickets)]
+                 1 if a["in_place"] else 0, a["passes"]]
+        ptrs = [_ptr(pv) for pv in (q, k, v, position, table, cache_k, cache_v, w, mask, out, out_k, out_v,
+                                    tickets, partials)]
         return kind, ptrs, ints, [a["divisor"]]
     if kind == K_GEMM:
         x, w = step.ins

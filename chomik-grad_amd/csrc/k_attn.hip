@@ -6,292 +6,345 @@
 //   K  = Kc * (1 - w) + k' * w   V  = Vc * (1 - w) + v * w
 //   o  = softmax(q' K^T / sqrt(hd) + mask) V        (query head h uses KV
 //                                                     head h / (H / KV))
-// with the portable graph's float16/bfloat16 rounding points (k_llama.hip
-// documents each).  Rows with w != 0 are blended on the fly from the old
-// cache values, so the result holds for any write mask.
+// RoPE, the blended cache rows and the scores keep the portable graph's
+// float16/bfloat16 rounding points:
+//   s = round(round(round(q'.k) / round(sqrt(hd))) + mask)
+// The softmax and P V are computed in float32 (the maximum, exp(s - m), their
+// sum and the weighted sum of V rows, divided once and rounded once), which
+// stays within the decode tolerance of the rounded portable chain.
 //
-// Latency, not bandwidth, bounds this kernel at batch 1 (a layer reads under
-// 1 MB), so every global load that does not depend on the position -- q, k,
-// v, the whole K and V block of the cache, the masks -- is issued before the
-// first wait; only the RoPE table lookup waits for the position.  Caches up
-// to kChunk rows are held in registers; longer ones are streamed in chunks.
+// Work split (split-context, "flash decoding"): one 256-thread workgroup per
+// (sequence, KV head, chunk of R cache rows).  It handles all G = H / KV query
+// heads of that KV head, so every cache row is read from memory once.  Each
+// workgroup writes its chunk's per-head maximum, exp-sum and unnormalised
+// P V to a partials buffer; the last workgroup of the (sequence, KV head) to
+// finish -- a self-resetting atomic ticket, no spinning -- combines the
+// (at most 64) chunks.  Every cache row belongs to exactly one workgroup, which reads it
+// and then (in place, when w != 0) writes the blended row: no other
+// workgroup touches it, so in-place updates are race free for any mask.
 //
-// Cache update:
-//  * in place (donated caches) with a 0/1 write mask: the first workgroup of
-//    each KV head writes the new rows.  Another workgroup may then read a
-//    row before or after that write; for w = 1 both give the new row.
-//  * in place with any other mask values: the last workgroup of the KV head
-//    to finish reading (self-resetting atomic ticket) writes the rows.
-//  * out of place: the H/KV workgroups of a KV head copy disjoint row sets.
-//
-// One 1024-thread workgroup per (sequence, query head); 8 lanes share one
-// 128-byte cache row (16-byte vectors), so a wave covers 8 rows per load.
+// 8 lanes (16 for float32) share one 128-byte row as 16-byte vectors; a
+// pass covers 32 (16) rows, and NP passes give R = 32 NP (16 NP) rows.  All
+// loads that do not depend on the position -- q, k, v, the chunk's K and V
+// rows, write-mask and attention-mask values -- are issued before the first
+// wait; only the RoPE table lookup waits for the position.
 #include "chip.h"
 #include "chomik_hip.h"
+
+#include <cstdlib>
 
 namespace chip {
 namespace {
 
 constexpr int kHead = 64;
-constexpr int kThreads = 1024;
-constexpr int kWaves = kThreads / 64;
+constexpr int kThreads = 256;
+constexpr int kMaxChunks = 64;  // cache chunks one (sequence, KV head) may split into
 
-template <bool MAX>
-__device__ __forceinline__ float block_reduce(float v, float* scratch) {
+__device__ __forceinline__ float nan_max(float a, float b) { return (b != b || b > a) ? b : a; }
+
+// Reduce-scatter of G per-head partial sums over the L lanes of a cache row
+// (lane index p within the row): at each butterfly step with offset o, while
+// a lane still holds more than one head it keeps one half of them (the upper
+// half when p & o) and adds the partner's copy of that half; once a single
+// head is left the remaining steps are a plain butterfly sum.  Lane p ends
+// with the full sum of head scatter_head(p).
+template <int G, int L>
+__device__ __forceinline__ int scatter_head(int p) {
+  int head = 0, held = G;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float other = __shfl_xor(v, o, 64);
-    v = MAX ? fmaxf(v, other) : v + other;
+  for (int o = L / 2; o >= 1; o >>= 1) {
+    if (held > 1) {
+      held >>= 1;
+      if (p & o) head += held;
+    }
   }
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float total = scratch[0];
+  return head;
+}
+template <int G, int L>
+__device__ __forceinline__ float reduce_scatter(float (&d)[G], int p) {
+  int held = G;
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) total = MAX ? fmaxf(total, scratch[w]) : total + scratch[w];
-  return total;
+  for (int o = L / 2; o >= 1; o >>= 1) {
+    if (held > 1) {
+      const int half = held >> 1;
+      const bool upper = (p & o) != 0;
+#pragma unroll
+      for (int i = 0; i < G / 2; ++i) {
+        if (i < half) {
+          const float send = upper ? d[i] : d[i + half];
+          const float keep = upper ? d[i + half] : d[i];
+          d[i] = keep + __shfl_xor(send, o, 64);
+        }
+      }
+      held = half;
+    } else {
+      d[0] += __shfl_xor(d[0], o, 64);
+    }
+  }
+  return d[0];
+}
+
+// The partials are exchanged between workgroups that may sit on different
+// XCDs (each with its own L2).  Agent-scope atomic stores and loads are
+// coherent across them without the whole-L2 writeback and invalidate that a
+// device-scope fence costs; the writer waits for its stores to complete
+// before it takes a ticket.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // p[0] q, p[1] k, p[2] v (linear outputs, strided views), p[3] positions
 // (int32), p[4] RoPE table (len, 64), p[5] K cache in, p[6] V cache in,
 // p[7] write mask, p[8] attention mask (or null), p[9] out (B, H, 1, 64),
-// p[10] K cache out, p[11] V cache out, p[12] tickets (B * KV int32, zero).
+// p[10] K cache out, p[11] V cache out, p[12] tickets (B * KV int32, zero),
+// p[13] partials (float32: B*H*NS*64 P V sums, then B*H*NS maxima, then
+// B*H*NS exp-sums; NS = ceil(C / R)).
 // n[0] B, n[1] H, n[2] KV, n[3] C, n[4] dtype, n[5..7] q strides (b, h, d),
 // n[8..10] k strides (b, g, d), n[11..13] v strides, n[14] position mode
 // (1 scalar, 2 per sequence), n[15] table length, n[16..19] cache strides
 // (b, g, c, d) (same for K and V), n[20..21] w strides (b, c), n[22..24]
 // mask strides (b, h, c), n[25] mask dtype, n[26] w dtype (both must be the
-// model dtype), n[27] in place;
+// model dtype), n[27] in place, n[28] passes per workgroup NP (1, 2 or 4);
 // f[0] score divisor (sqrt(hd) before rounding).
-template <typename T>
+template <typename T, int G, int NP>
 __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
   using E = Elem<T>;
   constexpr int V = 16 / static_cast<int>(sizeof(T));  // elements per vector
   constexpr int LPR = kHead / V;                        // lanes per row
-  constexpr int RPW = 64 / LPR;                         // rows per wave
-  constexpr int ROWS = kWaves * RPW;                    // rows per pass
-  constexpr int NP = sizeof(T) == 4 ? 3 : 6;            // passes held in registers
-  constexpr int kChunk = ROWS * NP;
+  constexpr int RPP = kThreads / LPR;                   // rows per pass
+  constexpr int R = RPP * NP;                           // rows per workgroup
+  constexpr int QT = (G * kHead + kThreads - 1) / kThreads;  // q values per thread
 
-  extern __shared__ float scores[];  // C floats
-  __shared__ float qs[kHead], ks[kHead], vs[kHead];
-  __shared__ float red[kWaves];
-  __shared__ float part[kWaves][kHead];
-  __shared__ int ticket;
-  __shared__ int odd_mask;
-  constexpr int kMaxList = 1024;      // rows with w != 0 remembered for the writer
-  __shared__ int nz_rows[kMaxList];
-  __shared__ int nz_count;
+  __shared__ float qs[G][kHead];
+  __shared__ float ks[kHead], vs[kHead];
+  __shared__ float es[G][R];
+  __shared__ float vsh[R][kHead];
+  __shared__ float red[kThreads / 64][G], red2[kThreads / 64][G];
+  __shared__ float mh[G], lh[G];
+  __shared__ float fac[G][kMaxChunks];
+  __shared__ int last;
 
-  const int64_t H = a.n[1], KV = a.n[2], C = a.n[3];
-  const int64_t G = H / KV;
-  const int64_t b = blockIdx.x / H, h = blockIdx.x % H, g = h / G;
+  const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
+  const int64_t NS = (C + R - 1) / R;
+  const int64_t split = blockIdx.x % NS, bg = blockIdx.x / NS;
+  const int64_t b = bg / KV, g = bg % KV;
   const int dt = E::code;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int slot = lane / LPR, chunk = lane % LPR;
+  const int rg = tid / LPR, part = tid % LPR;
+  const int64_t c0 = split * R;
   const T* Kc = static_cast<const T*>(a.p[5]);
   const T* Vc = static_cast<const T*>(a.p[6]);
   const int64_t cb = b * a.n[16] + g * a.n[17], cs = a.n[18];
   const int64_t wb = b * a.n[20], wc = a.n[21];
-  const int64_t mb = b * a.n[22] + h * a.n[23], mc = a.n[24];
+  const int64_t mb = b * a.n[22], mhs = a.n[23], mc = a.n[24];
   const bool masked = a.p[8] != nullptr;
   const bool in_place = a.n[27] != 0;
-  const T* Wm = static_cast<const T*>(a.p[7]);  // write mask (model dtype)
-  const T* Am = static_cast<const T*>(a.p[8]);  // attention mask (model dtype)
-  const int64_t row0 = wave * RPW + slot;  // first row of this lane group
+  const T* Wm = static_cast<const T*>(a.p[7]);
+  const T* Am = static_cast<const T*>(a.p[8]);
 
-  // -- issue: position, q/k/v, and the first chunk of K, V, w and mask.
+  // -- issue: position, q/k/v, this chunk's K and V rows, w and mask values.
   const int32_t* positions = static_cast<const int32_t*>(a.p[3]);
   int64_t pos = a.n[14] == 2 ? positions[b] : positions[0];
-  float xq = 0.f, xk = 0.f, xv = 0.f;
+  float xq[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;
+    xq[t] = i < G * kHead ? load_f(a.p[0], b * a.n[5] + (g * G + i / kHead) * a.n[6] + lane * a.n[7], dt) : 0.f;
+  }
+  float xk = 0.f, xv = 0.f;
   if (tid < kHead) {
-    xq = load_f(a.p[0], b * a.n[5] + h * a.n[6] + tid * a.n[7], dt);
     xk = load_f(a.p[1], b * a.n[8] + g * a.n[9] + tid * a.n[10], dt);
     xv = load_f(a.p[2], b * a.n[11] + g * a.n[12] + tid * a.n[13], dt);
   }
+  // the head whose scores this lane finishes (see reduce_scatter)
+  const int head = scatter_head<G, LPR>(part);
   uint4 kraw[NP], vraw[NP];
-  float wj[NP], mj[NP];
-  auto load_chunk = [&](int64_t base) {
+  float wj[NP], mk[NP];
 #pragma unroll
-    for (int u = 0; u < NP; ++u) {
-      const int64_t j = base + row0 + u * ROWS;
-      const bool in = j < C;
-      const int64_t off = cb + (in ? j : 0) * cs;
-      kraw[u] = in ? reinterpret_cast<const uint4*>(Kc + off)[chunk] : make_uint4(0, 0, 0, 0);
-      wj[u] = in ? E::to_f(Wm[wb + j * wc]) : 0.f;
-      mj[u] = (in && masked) ? E::to_f(Am[mb + j * mc]) : 0.f;
-    }
-  };
-  // V of a chunk (and its write-mask values, for the multi-chunk pass).
-  auto load_v = [&](int64_t base, bool with_mask) {
-#pragma unroll
-    for (int u = 0; u < NP; ++u) {
-      const int64_t j = base + row0 + u * ROWS;
-      const bool in = j < C;
-      vraw[u] = in ? reinterpret_cast<const uint4*>(Vc + cb + j * cs)[chunk] : make_uint4(0, 0, 0, 0);
-      if (with_mask) wj[u] = in ? E::to_f(Wm[wb + j * wc]) : 0.f;
-    }
-  };
-  load_chunk(0);
+  for (int u = 0; u < NP; ++u) {
+    const int64_t j = c0 + rg + u * RPP;
+    const bool in = j < C;
+    const int64_t off = cb + (in ? j : 0) * cs;
+    kraw[u] = in ? reinterpret_cast<const uint4*>(Kc + off)[part] : make_uint4(0, 0, 0, 0);
+    vraw[u] = in ? reinterpret_cast<const uint4*>(Vc + off)[part] : make_uint4(0, 0, 0, 0);
+    wj[u] = in ? E::to_f(Wm[wb + j * wc]) : 0.f;
+    mk[u] = (in && masked) ? E::to_f(Am[mb + (g * G + head) * mhs + j * mc]) : 0.f;
+  }
 
   // -- RoPE (waits for the position, then the table).
-  const bool pos_ok = pos >= 0 && pos < a.n[15];
-  if (!pos_ok) {
+  if (!(pos >= 0 && pos < a.n[15])) {
     if (tid == 0) raise_error(a, ERR_POSITION);
     pos = 0;
   }
-  if (tid == 0) {
-    odd_mask = 0;
-    nz_count = 0;
-  }
-  if (tid < kHead) {
-    const int i = tid & 31;
+  {
+    const int i = lane & 31;
     const float c = load_f(a.p[4], pos * kHead + i, dt);
     const float s = load_f(a.p[4], pos * kHead + 32 + i, dt);
-    const float pq = __shfl_xor(xq, 32, 64), pk = __shfl_xor(xk, 32, 64);
-    // lane d < 32 holds x[i] (partner x[i + 32]); lane d >= 32 holds x[i + 32]
-    const float rq = tid < 32 ? __fadd_rn(__fmul_rn(xq, c), __fmul_rn(pq, -s))
-                              : __fadd_rn(__fmul_rn(pq, s), __fmul_rn(xq, c));
-    const float rk = tid < 32 ? __fadd_rn(__fmul_rn(xk, c), __fmul_rn(pk, -s))
-                              : __fadd_rn(__fmul_rn(pk, s), __fmul_rn(xk, c));
-    qs[tid] = E::round(rq);
-    ks[tid] = E::round(rk);
-    vs[tid] = xv;
+    // lane d < 32 holds x[d] (partner x[d + 32]); lane d >= 32 holds x[d]
+    auto rope = [&](float x) {
+      const float p = __shfl_xor(x, 32, 64);
+      return E::round(lane < 32 ? __fadd_rn(__fmul_rn(x, c), __fmul_rn(p, -s))
+                                : __fadd_rn(__fmul_rn(p, s), __fmul_rn(x, c)));
+    };
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int i2 = tid + kThreads * t;
+      const float r = rope(xq[t]);
+      if (i2 < G * kHead) qs[i2 / kHead][lane] = r;
+    }
+    const float rk = rope(xk);
+    if (tid < kHead) {
+      ks[tid] = rk;
+      vs[tid] = xv;
+    }
   }
   __syncthreads();
-  float qv[V];
-#pragma unroll
-  for (int e = 0; e < V; ++e) qv[e] = qs[chunk * V + e];
-  const float* kn = ks + chunk * V;
-  const float* vn = vs + chunk * V;
-  const float div = E::round(a.f[0]);
 
-  // -- scores for one chunk held in kraw/wj/mj.
-  float local_max = -INFINITY;
-  bool odd = false;
-  auto score_chunk = [&](int64_t base) {
+  float qv[G][V];
 #pragma unroll
-    for (int u = 0; u < NP; ++u) {
-      const int64_t j = base + row0 + u * ROWS;
-      float kvals[V];
-      unpack<T>(kraw[u], kvals);
-      const float w = wj[u];
-      odd = odd || (w != 0.f && w != 1.f);
-      const float keep = E::round(1.f - w);
-      float dot = 0.f;
+  for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        float kd = kvals[e];
-        if (w != 0.f) kd = E::round(E::round(kd * keep) + E::round(kn[e] * w));
-        dot = fmaf(qv[e], kd, dot);
-      }
-#pragma unroll
-      for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
-      if (j < C) {
-        float s = E::round(E::round(dot) / div);
-        if (masked) s = E::round(s + mj[u]);
-        if (chunk == 0) {
-          scores[j] = s;
-          if (w != 0.f) {
-            const int at = atomicAdd(&nz_count, 1);
-            if (at < kMaxList) nz_rows[at] = static_cast<int>(j);
-          }
-        }
-        local_max = (s != s || s > local_max) ? s : local_max;
-      }
-      // keep each row's unpacked values short-lived (bounded register use)
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  const bool single = C <= kChunk;
-  score_chunk(0);
-  for (int64_t base = kChunk; base < C; base += kChunk) {
-    load_chunk(base);
-    score_chunk(base);
-  }
-  if (single) load_v(0, false);  // in flight during the reductions below
-  if (odd) odd_mask = 1;  // benign race: every writer stores 1
-  const float m = block_reduce<true>(local_max, red);
-  float local_sum = 0.f;
-  for (int64_t j = tid; j < C; j += kThreads) {
-    const float e = E::round(expf(E::round(scores[j] - m)));
-    scores[j] = e;
-    local_sum += e;
-  }
-  const float S = E::round(block_reduce<false>(local_sum, red));  // also orders scores[]
-
-  // -- out = sum_j round(e_j / S) * V_j.
-  float acc[V];
-#pragma unroll
-  for (int e = 0; e < V; ++e) acc[e] = 0.f;
-  auto pv_chunk = [&](int64_t base) {
-#pragma unroll
-    for (int u = 0; u < NP; ++u) {
-      const int64_t j = base + row0 + u * ROWS;
-      if (j >= C) break;
-      float vvals[V];
-      unpack<T>(vraw[u], vvals);
-      const float w = wj[u];
-      const float keep = E::round(1.f - w);
-      const float p = E::round(scores[j] / S);
-#pragma unroll
-      for (int e = 0; e < V; ++e) {
-        float vd = vvals[e];
-        if (w != 0.f) vd = E::round(E::round(vd * keep) + E::round(vn[e] * w));
-        acc[e] = fmaf(p, vd, acc[e]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  if (single) {
-    pv_chunk(0);
-  } else {
-    for (int64_t base = 0; base < C; base += kChunk) {
-      load_v(base, true);
-      pv_chunk(base);
-    }
-  }
+    for (int e = 0; e < V; ++e) qv[h][e] = qs[h][part * V + e];
+  float kn[V], vn[V];
 #pragma unroll
   for (int e = 0; e < V; ++e) {
-#pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) acc[e] += __shfl_xor(acc[e], o, 64);
+    kn[e] = ks[part * V + e];
+    vn[e] = vs[part * V + e];
   }
-  if (slot == 0) {
+  const float div = E::round(a.f[0]);
+
+  // -- scores of this lane group's rows.  The LPR lanes of a row each hold
+  // partial dot products for all G heads; a reduce-scatter over them (each
+  // step halves the heads a lane keeps) leaves every lane with one head's
+  // full dot product, so the rounding, division and mask are done once per
+  // (row, head) instead of once per lane.
+  float sc[NP];
+  float mloc = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < V; ++e) part[wave][chunk * V + e] = acc[e];
+  for (int u = 0; u < NP; ++u) {
+    const int64_t j = c0 + rg + u * RPP;
+    float kf[V];
+    unpack<T>(kraw[u], kf);
+    const float w = wj[u];
+    if (w != 0.f) {
+      const float keep = E::round(1.f - w);
+#pragma unroll
+      for (int e = 0; e < V; ++e) kf[e] = E::round(E::round(kf[e] * keep) + E::round(kn[e] * w));
+    }
+    float d[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) dot = fmaf(qv[h][e], kf[e], dot);
+      d[h] = dot;
+    }
+    const float dot = reduce_scatter<G, LPR>(d, part);
+    float s = E::round(E::round(dot) / div);
+    if (masked) s = E::round(s + mk[u]);
+    s = j < C ? s : -INFINITY;
+    sc[u] = s;
+    mloc = nan_max(mloc, s);
   }
+  // chunk maximum of this lane's head: across the wave's row groups, then
+  // the waves (lanes of row group 0 publish one value per head)
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) mloc = nan_max(mloc, __shfl_xor(mloc, o, 64));
+  if (lane < LPR) red[wave][head] = mloc;
   __syncthreads();
-  if (tid < kHead) {
-    float total = 0.f;
+  float m = red[0][head];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) total += part[w][tid];
-    static_cast<T*>(a.p[9])[(b * H + h) * kHead + tid] = E::from_f(total);
+  for (int w = 1; w < kThreads / 64; ++w) m = nan_max(m, red[w][head]);
+
+  // -- e = exp(s - m) per row of this lane's head; blended V rows into LDS.
+  float lsum = 0.f;
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const int64_t j = c0 + rg + u * RPP;
+    const int r = rg + u * RPP;
+    const float e = j < C ? __expf(sc[u] - m) : 0.f;
+    lsum += e;
+    es[head][r] = e;  // lanes sharing a head store the same value
+    float vf[V];
+    unpack<T>(vraw[u], vf);
+    const float w = wj[u];
+    if (w != 0.f) {
+      const float keep = E::round(1.f - w);
+#pragma unroll
+      for (int e2 = 0; e2 < V; ++e2) vf[e2] = E::round(E::round(vf[e2] * keep) + E::round(vn[e2] * w));
+    }
+#pragma unroll
+    for (int e2 = 0; e2 < V; ++e2) vsh[r][part * V + e2] = vf[e2];
+  }
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o, 64);
+  if (lane < LPR) red2[wave][head] = lsum;
+  __syncthreads();  // es, vsh, red, red2 complete
+  if (tid < G) {
+    float mm = red[0][tid], ll = red2[0][tid];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) {
+      mm = nan_max(mm, red[w][tid]);
+      ll += red2[w][tid];
+    }
+    mh[tid] = mm;
+    lh[tid] = ll;
   }
 
-  // -- cache update.
-  const int64_t hg = h % G;
-  if (in_place) {
-    if (odd_mask) {  // general mask: the last reader of this KV head writes
-      if (tid == 0) {
-        int* tickets = static_cast<int*>(a.p[12]);
-        __threadfence();
-        ticket = atomicAdd(&tickets[b * KV + g], 1);
-        if (ticket == G - 1) tickets[b * KV + g] = 0;  // reset for the next launch
+  // -- unnormalised P V of this chunk: thread (h, d) sums over the R rows.
+  float acc[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;
+    const int h = (i / kHead) < G ? i / kHead : 0;
+    float sum = 0.f;
+#pragma unroll 8
+    for (int r = 0; r < R; ++r) sum = fmaf(es[h][r], vsh[r][lane], sum);
+    acc[t] = sum;
+  }
+  __syncthreads();  // lh visible
+
+  float* partials = static_cast<float*>(a.p[13]);
+  const int64_t total = B * H * NS;
+  T* out = static_cast<T*>(a.p[9]);
+  if (NS == 1) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int i = tid + kThreads * t;
+      if (i < G * kHead) {
+        const int h = i / kHead;
+        out[(b * H + g * G + h) * kHead + lane] = E::from_f(acc[t] / lh[h]);
       }
-      __syncthreads();
-      if (ticket != G - 1) return;
-    } else if (hg != 0) {
-      return;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int i = tid + kThreads * t;
+      if (i < G * kHead) {
+        const int64_t row = (b * H + g * G + i / kHead) * NS + split;
+        store_agent(partials + row * kHead + lane, acc[t]);
+      }
+    }
+    if (tid < G) {
+      const int64_t row = (b * H + g * G + tid) * NS + split;
+      store_agent(partials + total * kHead + row, mh[tid]);
+      store_agent(partials + total * (kHead + 1) + row, lh[tid]);
     }
   }
+
+  // -- cache update for this chunk's rows (read above by this lane only).
   T* Ko = static_cast<T*>(a.p[10]);
   T* Vo = static_cast<T*>(a.p[11]);
-  // One lane group (LPR lanes, 16 bytes each) per row.
-  auto write_row = [&](int64_t j, float w) {
-    const int64_t src = cb + j * cs;
-    const int64_t dst = in_place ? src : ((b * KV + g) * C + j) * kHead;
-    uint4 kvec = reinterpret_cast<const uint4*>(Kc + src)[chunk];
-    uint4 vvec = reinterpret_cast<const uint4*>(Vc + src)[chunk];
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const int64_t j = c0 + rg + u * RPP;
+    if (j >= C) continue;
+    const float w = wj[u];
+    if (in_place && w == 0.f) continue;
+    uint4 kvec = kraw[u], vvec = vraw[u];
     if (w != 0.f) {
       const float keep = E::round(1.f - w);
       float kf[V], vf[V];
@@ -305,27 +358,104 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
       kvec = pack<T>(kf);
       vvec = pack<T>(vf);
     }
-    reinterpret_cast<uint4*>(Ko + dst)[chunk] = kvec;
-    reinterpret_cast<uint4*>(Vo + dst)[chunk] = vvec;
-  };
-  const int group = tid / LPR;
-  constexpr int kGroups = kThreads / LPR;
-  if (in_place) {
-    const int count = nz_count;  // ordered by the barriers above
-    if (count <= kMaxList) {
-      for (int r = group; r < count; r += kGroups) {
-        const int64_t j = nz_rows[r];
-        write_row(j, E::to_f(Wm[wb + j * wc]));
-      }
-    } else {
-      for (int64_t j = group; j < C; j += kGroups) {
-        const float w = E::to_f(Wm[wb + j * wc]);
-        if (w != 0.f) write_row(j, w);
-      }
-    }
-  } else {
-    for (int64_t j = hg + G * group; j < C; j += G * kGroups) write_row(j, E::to_f(Wm[wb + j * wc]));
+    const int64_t dst = in_place ? cb + j * cs : ((b * KV + g) * C + j) * kHead;
+    reinterpret_cast<uint4*>(Ko + dst)[part] = kvec;
+    reinterpret_cast<uint4*>(Vo + dst)[part] = vvec;
   }
+  if (NS == 1) return;
+
+  // -- the last workgroup of (b, g) to finish combines the chunks.
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();                // ... and every other thread's
+  if (tid == 0) {
+    int* tickets = static_cast<int*>(a.p[12]);
+    const int ticket = __hip_atomic_fetch_add(&tickets[b * KV + g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = ticket == static_cast<int>(NS) - 1;
+    if (last)  // reset for the next launch
+      __hip_atomic_store(&tickets[b * KV + g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  // Every partial load is issued before the first use (one round trip) and
+  // without branches (chunk indices clamped; the extra terms get factor 0):
+  // first the chunk maxima and exp-sums (one wave per head, one lane per
+  // chunk), then this thread's P V sums.
+  constexpr int HW = (G + kThreads / 64 - 1) / (kThreads / 64);  // heads per wave
+  const int64_t head0 = (b * H + g * G) * NS;
+  const int nlast = static_cast<int>(NS) - 1;
+  const int kc = lane < nlast ? lane : nlast;
+  float mk_[HW], lk_[HW];
+#pragma unroll
+  for (int x = 0; x < HW; ++x) {
+    const int h = wave + (kThreads / 64) * x;
+    const int64_t at = head0 + (h < G ? h : 0) * NS + kc;
+    mk_[x] = load_agent(partials + total * kHead + at);
+    lk_[x] = load_agent(partials + total * (kHead + 1) + at);
+  }
+  float ov[QT][kMaxChunks];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;
+    const int h = (i / kHead) < G ? i / kHead : 0;
+    const float* Op = partials + (head0 + h * NS) * kHead + lane;
+#pragma unroll
+    for (int k0 = 0; k0 < kMaxChunks; k0 += 8) {
+      if (k0 >= NS) break;  // uniform: only the blocks of 8 chunks that exist
+#pragma unroll
+      for (int k = k0; k < k0 + 8; ++k) ov[t][k] = load_agent(Op + (k < nlast ? k : nlast) * kHead);
+    }
+  }
+  // per head: m = max over chunks; weights exp(M_k - m) / sum_k L_k exp(M_k - m)
+#pragma unroll
+  for (int x = 0; x < HW; ++x) {
+    const int h = wave + (kThreads / 64) * x;
+    if (h >= G) break;
+    const float mk = lane < NS ? mk_[x] : -INFINITY;
+    float m = mk;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = nan_max(m, __shfl_xor(m, o, 64));
+    const float f = lane < NS ? __expf(mk - m) : 0.f;
+    float l = lane < NS ? lk_[x] * f : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    fac[h][lane] = f / l;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;
+    if (i >= G * kHead) continue;
+    const float* F = fac[i / kHead];
+    float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k0 = 0; k0 < kMaxChunks; k0 += 8) {
+      if (k0 >= NS) break;
+#pragma unroll
+      for (int k = k0; k < k0 + 8; ++k) o4[k & 3] = fmaf(ov[t][k], F[k], o4[k & 3]);
+    }
+    out[(b * H + g * G + i / kHead) * kHead + lane] = E::from_f((o4[0] + o4[1]) + (o4[2] + o4[3]));
+  }
+}
+
+template <typename T, int G>
+const void* pick_np(int np) {
+  switch (np) {
+    case 1: return reinterpret_cast<const void*>(&k_decode_attn<T, G, 1>);
+    case 2: return reinterpret_cast<const void*>(&k_decode_attn<T, G, 2>);
+    case 4: return reinterpret_cast<const void*>(&k_decode_attn<T, G, 4>);
+  }
+  return nullptr;
+}
+
+template <typename T>
+const void* pick_g(int64_t G, int np) {
+  switch (G) {
+    case 1: return pick_np<T, 1>(np);
+    case 2: return pick_np<T, 2>(np);
+    case 4: return pick_np<T, 4>(np);
+    case 8: return pick_np<T, 8>(np);
+  }
+  return nullptr;
 }
 
 const char* plan_decode_attn(KArgs& a, Launch& l) {
@@ -334,20 +464,23 @@ const char* plan_decode_attn(KArgs& a, Launch& l) {
   if (a.n[18] != kHead || a.n[19] != 1) return "decode_attn: cache rows must be contiguous 64-element rows";
   if (a.n[14] != 1 && a.n[14] != 2) return "decode_attn: position input required";
   if (a.n[25] != a.n[4] || a.n[26] != a.n[4]) return "decode_attn: masks must have the model dtype";
-  const size_t lds = static_cast<size_t>(C) * sizeof(float);
-  if (lds > 96 * 1024) return "decode_attn: cache longer than 24576 rows";
+  const int np = static_cast<int>(a.n[28]);
+  if (np != 1 && np != 2 && np != 4) return "decode_attn: passes per workgroup must be 1, 2 or 4";
+  if ((C + (a.n[4] == F32 ? 16 : 32) * np - 1) / ((a.n[4] == F32 ? 16 : 32) * np) > kMaxChunks)
+    return "decode_attn: more than 64 cache chunks per KV head";
   switch (a.n[4]) {
-    case F32: l.func = reinterpret_cast<const void*>(&k_decode_attn<float>); break;
-    case F16: l.func = reinterpret_cast<const void*>(&k_decode_attn<__half>); break;
-    case BF16: l.func = reinterpret_cast<const void*>(&k_decode_attn<bf16_t>); break;
+    case F32: l.func = pick_g<float>(H / KV, np); break;
+    case F16: l.func = pick_g<__half>(H / KV, np); break;
+    case BF16: l.func = pick_g<bf16_t>(H / KV, np); break;
     default: return "decode_attn: float dtype required";
   }
-  if (lds > 48 * 1024 &&
-      hipFuncSetAttribute(l.func, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
-    return "decode_attn: cannot raise the LDS limit";
-  l.grid = dim3(static_cast<unsigned>(B * H));
+  if (!l.func) return "decode_attn: query heads per KV head must be 1, 2, 4 or 8";
+  const int64_t rows = (a.n[4] == F32 ? 16 : 32) * np;
+  const int64_t blocks = B * KV * ((C + rows - 1) / rows);
+  if (blocks > 2147483647) return "decode_attn: too many workgroups";
+  l.grid = dim3(static_cast<unsigned>(blocks));
   l.block = dim3(kThreads);
-  l.shmem = lds;
+  l.shmem = 0;
   a.p[kErrPtr] = device_error_word();
   return nullptr;
 }

@@ -435,7 +435,8 @@ def s_decode_attn(mem, p, n, f):
     qs, ks, vs = n[5:8], n[8:11], n[11:14]
     mode, length = n[14], n[15]
     cs = n[16:20]
-    wsb, wsc, msb, msh, msc, mdt, wdt, in_place = n[20:28]
+    wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes = n[20:29]
+    assert passes in (1, 2, 4)
     G = H // KV
     div = _round(np.float32(f[0]), dt)
     error = 0
@@ -468,9 +469,9 @@ def s_decode_attn(mem, p, n, f):
                     sc = _round(_round((Kn.astype(np.float64) @ q).astype(np.float32), dt) / div, dt)
                     if p[8][0] >= 0:
                         sc = _round(sc + load(mem, p[8], mdt, b * msb + h * msh + np.arange(C) * msc), dt)
-                    e = _round(np.exp(_round(sc - sc.max(), dt)), dt)
-                    S = _round(e.sum(), dt)
-                    out = (_round(e / S, dt).astype(np.float64) @ Vn).astype(np.float32)
+                    # float32 softmax and P V (one division, one rounding)
+                    e = np.exp(sc.astype(np.float64) - np.float64(sc.max()))
+                    out = ((e @ Vn.astype(np.float64)) / e.sum()).astype(np.float32)
                     store(mem, p[9], dt, (b * H + h) * 64 + d, out)
     for (b, g), (idx, Kn, Vn, w) in newk.items():
         if in_place:

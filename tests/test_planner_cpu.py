@@ -24,6 +24,7 @@ from chomikgrad.llama import (
     position_selector,
 )
 from conftest import tiny_weights
+import attention_cases
 from tape_model import CpuPlanCompiler, run
 
 COMPILER = CpuPlanCompiler()
@@ -122,7 +123,7 @@ def _fp16_layer():
     return config, synthetic.weights_as_tensors(host)
 
 
-def test_fp16_decode_step_is_bit_exact_with_oracle_roundings():
+def test_fp16_decode_step_matches_oracle_roundings():
     config, weights = _fp16_layer()
     C, position = 24, 11
     rng = np.random.default_rng(4)
@@ -136,12 +137,11 @@ def test_fp16_decode_step_is_bit_exact_with_oracle_roundings():
     outputs = dec(*leaves[:4], [(caches[0], caches[1])], position=leaves[4])
     expected = realize(*outputs, compiler="cpu")
     _, got = model_run(outputs, leaves + caches)
-    # The fused kernels round where the portable graph rounds; only the
-    # order of float32 sums differs.  An occasional one-ulp flip in the hidden
-    # state moves many logits by an ulp, but most stay bit-identical (without
-    # the matching roundings almost none would).
+    # The fused kernels round where the portable graph rounds, except the
+    # decode attention's softmax and P V, which run in float32 and round once;
+    # the order of float32 sums differs too.  The logits stay within a few
+    # float16 ulps; the cache rows (RoPE and the blended write) stay exact.
     np.testing.assert_allclose(got[0].astype(np.float32), expected[0].astype(np.float32), atol=2e-3, rtol=2e-3)
-    assert np.mean(got[0] == expected[0]) > 0.5
     for value, reference in zip(got[1:], expected[1:]):
         np.testing.assert_allclose(value.astype(np.float32), reference.astype(np.float32), atol=2e-3, rtol=1e-2)
         assert np.mean(value == reference) > 0.99
@@ -261,3 +261,21 @@ def test_memory_plan_reuses_the_arena():
     planned = plan_graph(COMPILER, [y._node], [])
     per_value = 64 * 64 * 4
     assert planned.arena_bytes <= 3 * per_value
+
+
+@pytest.mark.parametrize("passes", [0, 1, 2, 4])
+@pytest.mark.parametrize("case", [c for c in attention_cases.CASES if c.C * c.B <= 1000], ids=lambda c: c.name)
+def test_decode_attention_fusion_matches_oracle(case, passes, monkeypatch):
+    """The fused decode attention (split over cache chunks, combined by the
+    last workgroup) against the portable chain on the oracle; caches exact."""
+    from chomikgrad import _planner
+
+    monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", passes)
+    outputs, dynamic, caches = attention_cases.build(case)
+    expected = realize(*outputs, compiler="cpu")
+    for donate in ((), caches):
+        planned, got = model_run(outputs, dynamic, donate=donate)
+        assert [s.kind for s in planned.steps].count(K_DECODE_ATTN) == 1
+        np.testing.assert_allclose(as_float(got[0]), as_float(expected[0]), **attention_cases.tolerance(case))
+        for value, reference in zip(got[1:], expected[1:]):
+            np.testing.assert_array_equal(np.asarray(value).view(np.uint8), np.asarray(reference).view(np.uint8))

@@ -32,6 +32,56 @@ namespace {
 // are 16-byte aligned (vector staging); f[0] eps.
 constexpr int kMaxRows = 8;
 
+// The weight segments of one launch, read from the kernel arguments by
+// constant index.  Indexing KArgs with a runtime value (a.p[2 + s]) compiles
+// to a memory load whose wait would also drain every weight load in flight,
+// so a row's segment is found by comparing with the cumulative row counts and
+// its pointers and strides are chosen with selects.
+template <typename T>
+struct Segments {
+  int64_t e0, e1, e2, total;  // cumulative row ends (INT64_MAX past the last segment)
+  const T* w[4];
+  T* out[4];
+  const T* res[4];
+  int64_t ostride[4], rstride[4];
+
+  template <typename V>
+  __device__ static __forceinline__ V pick(int s, V v0, V v1, V v2, V v3) {
+    return s == 0 ? v0 : s == 1 ? v1 : s == 2 ? v2 : v3;
+  }
+  __device__ explicit Segments(const KArgs& a) {
+    const int segs = static_cast<int>(a.n[4]);
+    const int64_t big = INT64_MAX;
+    const int64_t c0 = a.n[7], c1 = c0 + a.n[8], c2 = c1 + a.n[9], c3 = c2 + a.n[10];
+    e0 = segs > 1 ? c0 : big;
+    e1 = segs > 2 ? c1 : big;
+    e2 = segs > 3 ? c2 : big;
+    total = segs == 1 ? c0 : segs == 2 ? c1 : segs == 3 ? c2 : c3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = static_cast<const T*>(a.p[2 + i]);
+      out[i] = static_cast<T*>(a.p[6 + i]);
+      res[i] = static_cast<const T*>(a.p[10 + i]);
+      ostride[i] = a.n[11 + i];
+      rstride[i] = a.n[15 + i];
+    }
+  }
+  __device__ int seg_of(int64_t g) const { return (g >= e0) + (g >= e1) + (g >= e2); }
+  __device__ int64_t start(int s) const { return pick(s, int64_t(0), e0, e1, e2); }
+  __device__ const T* weight(int s) const { return pick(s, w[0], w[1], w[2], w[3]); }
+  __device__ T* output(int s) const { return pick(s, out[0], out[1], out[2], out[3]); }
+  __device__ const T* residual(int s) const { return pick(s, res[0], res[1], res[2], res[3]); }
+  __device__ int64_t out_stride(int s) const { return pick(s, ostride[0], ostride[1], ostride[2], ostride[3]); }
+  __device__ int64_t res_stride(int s) const { return pick(s, rstride[0], rstride[1], rstride[2], rstride[3]); }
+  // residual element i of segment s without a branch (a branch's join would
+  // wait for every load in flight): a segment without one reads the input
+  // x[0] instead, which the caller discards
+  __device__ float load_residual(int s, int64_t i, const void* x) const {
+    const T* r = residual(s);
+    return Elem<T>::to_f(r ? r[i] : static_cast<const T*>(x)[0]);
+  }
+};
+
 template <typename T, int MM, int NR, int U, bool PRO, bool SILU, bool STAGE, int SPLIT>
 __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
   using E = Elem<T>;
@@ -54,6 +104,7 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
   const int64_t c_begin = slice * slice_len;
   const int64_t c_end = c_begin + slice_len < KV ? c_begin + slice_len : KV;
 
+  const Segments<T> st(a);
   // Weight rows of this wave.
   const uint4* wrow[NR];
   int seg[NR];
@@ -71,16 +122,11 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
   } else {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      int64_t g = wave * NR + r;
-      int s = 0;
-      while (s < a.n[4] && g >= a.n[7 + s]) {
-        g -= a.n[7 + s];
-        ++s;
-      }
-      valid[r] = s < a.n[4];
-      seg[r] = valid[r] ? s : 0;
-      idx[r] = valid[r] ? g : 0;
-      wrow[r] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2 + seg[r]]) + idx[r] * K);
+      const int64_t g = wave * NR + r;
+      valid[r] = g < st.total;
+      seg[r] = valid[r] ? st.seg_of(g) : 0;
+      idx[r] = valid[r] ? g - st.start(seg[r]) : 0;
+      wrow[r] = reinterpret_cast<const uint4*>(st.weight(seg[r]) + idx[r] * K);
     }
   }
 
@@ -126,11 +172,8 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      resv[m][r] = 0.f;
-      if (!SILU && m < M && valid[r] && a.p[10 + seg[r]])
-        resv[m][r] = E::to_f(static_cast<const T*>(a.p[10 + seg[r]])[m * a.n[15 + seg[r]] + idx[r]]);
-    }
+    for (int r = 0; r < NR; ++r)
+      resv[m][r] = (!SILU && m < M) ? st.load_residual(seg[r], m * st.res_stride(seg[r]) + idx[r], a.p[0]) : 0.f;
 
   T* xs_t = reinterpret_cast<T*>(xs);
   if (STAGE && x_in_regs) {
@@ -318,8 +361,8 @@ __global__ __launch_bounds__(256) void k_gemv(KArgs a) {
         if (!valid[r]) continue;
         const int s = seg[r];
         float y = E::round(acc[m][r]);
-        if (a.p[10 + s]) y = E::round(resv[m][r] + y);
-        static_cast<T*>(a.p[6 + s])[m * a.n[11 + s] + idx[r]] = E::from_f(y);
+        if (st.residual(s)) y = E::round(resv[m][r] + y);
+        st.output(s)[m * st.out_stride(s) + idx[r]] = E::from_f(y);
       }
     }
   }
@@ -430,7 +473,10 @@ __global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
   const int64_t K = a.n[1];
   const int KV = static_cast<int>(K / V);
   const int lane = threadIdx.x & 63;
-  const int64_t wave = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
+  // wave-uniform (scalar registers): the row arithmetic stays off the VGPRs
+  const int64_t wave = blockIdx.x * int64_t(blockDim.x >> 6) +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const Segments<T> st(a);
 
   const uint4* wrow[NR];
   int seg[NR];
@@ -447,16 +493,11 @@ __global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
   } else {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      int64_t g = wave * NR + r;
-      int s = 0;
-      while (s < a.n[4] && g >= a.n[7 + s]) {
-        g -= a.n[7 + s];
-        ++s;
-      }
-      valid[r] = s < a.n[4];
-      seg[r] = valid[r] ? s : 0;
-      idx[r] = valid[r] ? g : 0;
-      wrow[r] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2 + seg[r]]) + idx[r] * K);
+      const int64_t g = wave * NR + r;
+      valid[r] = g < st.total;
+      seg[r] = valid[r] ? st.seg_of(g) : 0;
+      idx[r] = valid[r] ? g - st.start(seg[r]) : 0;
+      wrow[r] = reinterpret_cast<const uint4*>(st.weight(seg[r]) + idx[r] * K);
     }
   }
   if (!valid[0]) return;  // rows are assigned in order: no valid row after an invalid one
@@ -468,14 +509,13 @@ __global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
   float acc[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = 0.f;
-  // the residual this row's writer adds, loaded ahead of the stream
+  // the residual this row's writer adds, issued first (the scheduling
+  // barrier keeps the compiler from sinking the load to its use, which would
+  // add a round trip after the reduction)
   float resv[NR];
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    resv[r] = 0.f;
-    if (!SILU && lane == 0 && valid[r] && a.p[10 + seg[r]])
-      resv[r] = E::to_f(static_cast<const T*>(a.p[10 + seg[r]])[idx[r]]);
-  }
+  for (int r = 0; r < NR; ++r) resv[r] = SILU ? 0.f : st.load_residual(seg[r], idx[r], a.p[0]);
+  __builtin_amdgcn_sched_barrier(0);
 
   for (int chunk = 0; chunk < chunks; ++chunk) {
     const int base = chunk * 64 * VPL + lane;
@@ -516,6 +556,9 @@ __global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
       }
     // rows of an invalid slot (NR > 1 tail) read row 0 of their segment and
     // contribute nothing: their results are never stored
+    // Keep the weight stream ahead of the prologue's arithmetic (the
+    // scheduler would otherwise sink the loads below it to save registers).
+    __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (kWord) {
       using W = Word<T>;
@@ -620,21 +663,207 @@ __global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
 
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
-  if (lane != 0) return;
+  // The epilogue runs on every lane and only the store is lane 0's: with the
+  // residual's use inside a lane-0 branch the compiler would sink its load
+  // to after the reduction, one more round trip at the end.
   if (SILU) {
     const float g = E::round(acc[0]);
     const float u = E::round(acc[1]);
     const float denom = E::round(E::round(expf(-g)) + 1.f);
-    static_cast<T*>(a.p[6])[idx[0]] = E::from_f(E::round(E::round(g / denom) * u));
+    const T y = E::from_f(E::round(E::round(g / denom) * u));
+    if (lane == 0) static_cast<T*>(a.p[6])[idx[0]] = y;
     return;
   }
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
-    if (!valid[r]) continue;
     const int s = seg[r];
     float y = E::round(acc[r]);
-    if (a.p[10 + s]) y = E::round(resv[r] + y);
-    static_cast<T*>(a.p[6 + s])[idx[r]] = E::from_f(y);
+    y = st.residual(s) ? E::round(resv[r] + y) : y;
+    const T out = E::from_f(y);
+    if (lane == 0 && valid[r]) st.output(s)[idx[r]] = out;
+  }
+}
+
+// Streaming decode GEMV (M = 1, 16-bit types, rows that are an exact fit:
+// K / 8 == 64 VPL).  n[23] waves each own a contiguous run of row groups (a
+// group is one output row, or the gate/up pair of the SiLU epilogue).  A wave
+// loads x (and the norm weight), issues its first group's weight rows,
+// computes the RMSNorm prologue once into registers, then walks its groups
+// with the next group's rows and residual in flight while the current group
+// is reduced.  The prologue -- the same arithmetic as k_gemv_row's -- is
+// thereby paid once per wave instead of once per row.  Same KArgs layout as
+// k_gemv, plus n[23] = number of waves.
+template <typename T, int VPL, bool PRO, bool SILU, bool NT>
+__global__ __launch_bounds__(256) void k_gemv_stream(KArgs a) {
+  using E = Elem<T>;
+  using W = Word<T>;
+  constexpr int RG = SILU ? 2 : 1;
+  const int64_t K = a.n[1];
+  const int lane = threadIdx.x & 63;
+  // wave-uniform (scalar registers): the row arithmetic stays off the VGPRs
+  const int64_t wave = blockIdx.x * int64_t(blockDim.x >> 6) +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t waves = a.n[23];
+  const int64_t groups = SILU ? a.n[7] : Segments<T>(a).total;
+  if (wave >= waves) return;
+  const int64_t g0 = wave * groups / waves, g1 = (wave + 1) * groups / waves;
+  if (g0 >= g1) return;
+
+  const Segments<T> st(a);
+  // weight row r of group g: its segment and the row within it
+  auto locate = [&](int64_t g, int r, int& seg, int64_t& idx) -> const uint4* {
+    if (SILU) {
+      seg = r;
+      idx = g;
+      return reinterpret_cast<const uint4*>((r == 0 ? st.w[0] : st.w[1]) + g * K);
+    }
+    seg = st.seg_of(g);
+    idx = g - st.start(seg);
+    return reinterpret_cast<const uint4*>(st.weight(seg) + idx * K);
+  };
+
+  const uint4* xg = static_cast<const uint4*>(a.p[0]);
+  const uint4* ng = static_cast<const uint4*>(a.p[1]);
+  uint4 xv[VPL], nv[PRO ? VPL : 1];
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) xv[u] = load_x(xg + lane + 64 * u);
+  if (PRO) {
+#pragma unroll
+    for (int u = 0; u < VPL; ++u) nv[u] = load_x(ng + lane + 64 * u);
+  }
+  // Two register buffers alternate between groups (a copy from one to the
+  // other would have to wait for the loads to land): while one group is
+  // reduced the next one's rows and residual are in flight.  The prefetch is
+  // unconditional -- past the last group it re-reads that group -- because a
+  // branch around the loads would make the wait before the math drain them.
+  struct Group {
+    uint4 w[RG][VPL];
+    int seg;
+    int64_t idx;
+    float res;
+  };
+  auto issue = [&](Group& b, int64_t g) {
+    const uint4* wp[RG];
+    int sg[RG];
+    int64_t ix[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) wp[r] = locate(g, r, sg[r], ix[r]);
+    b.seg = sg[0];
+    b.idx = ix[0];
+    b.res = SILU ? 0.f : st.load_residual(sg[0], ix[0], a.p[0]);
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) b.w[r][u] = load_w<NT>(wp[r] + lane + 64 * u);
+  };
+  Group A, B;
+  issue(A, g0);
+  __builtin_amdgcn_sched_barrier(0);  // the first rows stream during the prologue
+
+  uint32_t xw[VPL][4];
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) {
+    xw[u][0] = xv[u].x;
+    xw[u][1] = xv[u].y;
+    xw[u][2] = xv[u].z;
+    xw[u][3] = xv[u].w;
+  }
+  if (PRO) {
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < VPL; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[u][i], xw[u][i]), W::kOnes, ss);
+    const float total = E::round(wave_sum(ss));
+    const float mean = E::round(total / E::round(static_cast<float>(K)));
+    const float rn = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+    const float inv = 1.0f / rn;
+    bool fast = W::fast_divisor(rn);
+    if constexpr (!W::kNoBranch) {
+#pragma unroll
+      for (int u = 0; u < VPL; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          fast = fast && W::fast_numerator(W::lo(xw[u][i])) && W::fast_numerator(W::hi(xw[u][i]));
+      fast = __all(fast);
+    }
+#pragma unroll
+    for (int u = 0; u < VPL; ++u) {
+      const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = W::lo(xw[u][i]), hi = W::hi(xw[u][i]);
+        float ql, qh;
+        if constexpr (W::kNoBranch) {
+          ql = fast ? quotient(lo, rn, inv) : lo * inv;
+          qh = fast ? quotient(hi, rn, inv) : hi * inv;
+        } else {
+          ql = fast ? quotient(lo, rn, inv) : lo / rn;
+          qh = fast ? quotient(hi, rn, inv) : hi / rn;
+        }
+        xw[u][i] = W::mul(W::pack(ql, qh), nw[i]);
+      }
+    }
+  }
+
+  auto finish = [&](const Group& b) {
+    float acc[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const uint32_t ww[4] = {b.w[r][u].x, b.w[r][u].y, b.w[r][u].z, b.w[r][u].w};
+        s0 = W::dot(xw[u][0], ww[0], s0);
+        s1 = W::dot(xw[u][1], ww[1], s1);
+        s0 = W::dot(xw[u][2], ww[2], s0);
+        s1 = W::dot(xw[u][3], ww[3], s1);
+      }
+      acc[r] = wave_sum(s0 + s1);
+    }
+    if (lane == 0) {
+      if (SILU) {
+        const float gv = E::round(acc[0]);
+        const float uv = E::round(acc[1]);
+        const float denom = E::round(E::round(expf(-gv)) + 1.f);
+        st.out[0][b.idx] = E::from_f(E::round(E::round(gv / denom) * uv));
+      } else {
+        float y = E::round(acc[0]);
+        if (st.residual(b.seg)) y = E::round(b.res + y);
+        st.output(b.seg)[b.idx] = E::from_f(y);
+      }
+    }
+  };
+  for (int64_t g = g0; g < g1; g += 2) {
+    issue(B, g + 1 < g1 ? g + 1 : g);
+    finish(A);
+    if (g + 1 >= g1) break;
+    issue(A, g + 2 < g1 ? g + 2 : g + 1);
+    finish(B);
+  }
+}
+
+template <typename T, int VPL, bool NT>
+const void* pick_stream_kernel(bool pro, bool silu) {
+  if (silu)
+    return pro ? reinterpret_cast<const void*>(&k_gemv_stream<T, VPL, true, true, NT>)
+               : reinterpret_cast<const void*>(&k_gemv_stream<T, VPL, false, true, NT>);
+  return pro ? reinterpret_cast<const void*>(&k_gemv_stream<T, VPL, true, false, NT>)
+             : reinterpret_cast<const void*>(&k_gemv_stream<T, VPL, false, false, NT>);
+}
+
+// exact fits of the decode shapes: 512, 1024, 2048, 4096, 5632, 8192 columns
+template <typename T>
+const void* pick_stream(int64_t kv, bool pro, bool silu) {
+  if (kv % 64) return nullptr;
+  switch (kv / 64) {
+    case 1: return pick_stream_kernel<T, 1, true>(pro, silu);
+    case 2: return pick_stream_kernel<T, 2, true>(pro, silu);
+    case 4: return pick_stream_kernel<T, 4, true>(pro, silu);
+    case 8: return pick_stream_kernel<T, 8, true>(pro, silu);
+    case 11: return silu ? nullptr : pick_stream_kernel<T, 11, true>(pro, silu);
+    case 16: return (silu || pro) ? nullptr : pick_stream_kernel<T, 16, true>(pro, silu);
+    default: return nullptr;
   }
 }
 
@@ -733,6 +962,28 @@ const char* plan_gemv(KArgs& a, Launch& l) {
                                           per_lane == 8 || (per_lane == 11 && !silu))) ||
                         per_lane <= 4;
   const bool row_ok = M == 1 && aligned && (!pro || (a.n[19] == dt && one_pass));
+  // 0: never stream, 1: stream large matrices, 2: stream every exact fit
+  static const int stream_knob = env_int("CHOMIK_HIP_GEMV_STREAM", 1);
+  if (row_ok && stream_knob && (dt == F16 || dt == BF16)) {
+    const void* func = dt == F16 ? pick_stream<__half>(kv, pro, silu) : pick_stream<bf16_t>(kv, pro, silu);
+    // about eight waves per CU: as many row groups per wave as that takes,
+    // then as few waves as those groups need (balanced runs).  Only worth it
+    // from 8 groups per wave (the lm_head): below that one wave per row with
+    // every load issued at once (k_gemv_row) finishes sooner.
+    static const int target = env_int("CHOMIK_HIP_GEMV_TARGET_WAVES", 2048);
+    const int64_t groups = silu ? a.n[7] : rows;
+    const int64_t per_wave = (groups + target - 1) / target;
+    if (func && (per_wave >= 8 || stream_knob == 2)) {
+      const int64_t waves = (groups + per_wave - 1) / per_wave;
+      if ((waves + 3) / 4 > 2147483647) return "gemv: too many rows";
+      a.n[23] = waves;
+      l.func = func;
+      l.grid = dim3(static_cast<unsigned>((waves + 3) / 4));
+      l.block = dim3(256);
+      l.shmem = 0;
+      return nullptr;
+    }
+  }
   if (row_ok) {
     static const int waves_knob = env_int("CHOMIK_HIP_GEMV_WAVES", 0);
     static const int nt_knob = env_int("CHOMIK_HIP_GEMV_NT", 1);

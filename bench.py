@@ -118,8 +118,9 @@ def step_flops(step) -> int:
     (the causal triangle when the mask was proved causal)."""
     from chomikgrad._planner import K_GEMM, K_SDPA
 
-    if step.kind == K_GEMM:
-        return 2 * step.attrs["rows"] * step.attrs["N"] * step.attrs["K"]
+    if step.kind == K_GEMM:  # the SiLU pair multiplies by gate and up weights
+        pair = 2 if step.attrs.get("up") is not None else 1
+        return 2 * pair * step.attrs["rows"] * step.attrs["N"] * step.attrs["K"]
     if step.kind == K_SDPA:
         b, h, t, hd = step.ins[0].shape
         c = step.ins[1].shape[2]
@@ -133,7 +134,9 @@ def plan_label(step) -> str:
     from chomikgrad._planner import K_GEMM, KIND_NAMES
 
     if step.kind == K_GEMM:
-        return f"gemm {step.attrs['rows']}x{step.attrs['N']}x{step.attrs['K']}"
+        epilogue = "+silu_pair" if step.attrs.get("up") is not None else (
+            "+residual" if step.attrs.get("res") is not None else "")
+        return f"gemm{epilogue} {step.attrs['rows']}x{step.attrs['N']}x{step.attrs['K']}"
     return kernel_label(step)
 
 

@@ -912,6 +912,71 @@ def fuse_residual(steps: List[Step], outputs: List[PV]) -> List[Step]:
     return [s for s in steps if id(s) not in removed]
 
 
+def fuse_gemm_epilogues(steps: List[Step], outputs: List[PV]) -> List[Step]:
+    """Prefill: ``silu(g) * u`` of two GEMMs over the same input -> one GEMM
+    with both weights and the SiLU epilogue; ``h + y`` of a GEMM output ->
+    the GEMM's residual epilogue (the GEMV fusions, for many rows)."""
+    counts = _consumers(steps, outputs)
+    producer = _producer(steps)
+    removed = set()
+    for step in steps:
+        if step.kind != K_ELEMENTWISE or not step.attrs.get("silu_mul"):
+            continue
+        g, u = step.ins[0], step.ins[1]
+        pg, pu = producer.get(id(g.storage)), producer.get(id(u.storage))
+        if not pg or not pu:
+            continue
+        gs, us = pg[1], pu[1]
+        if gs.kind != K_GEMM or us.kind != K_GEMM or gs is us or gs.attrs.get("res") or us.attrs.get("res"):
+            continue
+        if not gs.ins[0].same_data(us.ins[0]) or gs.attrs["N"] != us.attrs["N"] or gs.attrs["K"] != us.attrs["K"]:
+            continue
+        if counts.get(id(g.storage)) != 1 or counts.get(id(u.storage)) != 1 or not (g.whole() and u.whole()):
+            continue
+        out = step.outs[0]
+        if not out.whole() or _prod(out.shape) != gs.attrs["rows"] * gs.attrs["N"]:
+            continue
+        gs.attrs["up"] = us.ins[1]
+        gs.ins = [gs.ins[0], gs.ins[1], us.ins[1]]
+        gs.outs = [out]
+        removed.update({id(us), id(step)})
+    steps = [s for s in steps if id(s) not in removed]
+    counts = _consumers(steps, outputs)
+    producer = _producer(steps)
+    removed = set()
+    for step in steps:
+        if step.kind != K_ELEMENTWISE or step.attrs.get("silu_mul"):
+            continue
+        expression = step.attrs["expression"]
+        if not (expression[0] == "add" and len(expression) == 4 and expression[2][0] == "input"
+                and expression[3][0] == "input" and len(step.ins) == 2):
+            continue
+        out = step.outs[0]
+        for y_index in (1, 0):
+            y, h = step.ins[y_index], step.ins[1 - y_index]
+            found = producer.get(id(y.storage))
+            if not found:
+                continue
+            gemm_index, gemm = found
+            if gemm.kind != K_GEMM or gemm.attrs.get("up") is not None or gemm.attrs.get("res") is not None:
+                continue
+            h_producer = producer.get(id(h.storage))
+            if h_producer is not None and h_producer[0] >= gemm_index:
+                continue
+            if counts.get(id(y.storage)) != 1 or not y.whole() or not out.whole():
+                continue
+            if h.shape != out.shape or not h.contiguous() or h.dtype != out.dtype or y.dtype != out.dtype:
+                continue
+            if _prod(out.shape) != gemm.attrs["rows"] * gemm.attrs["N"] or h.offset % 8:
+                continue
+            gemm.attrs["res"] = h
+            gemm.ins = gemm.ins + [h]
+            gemm.outs = [out]
+            removed.add(id(step))
+            break
+    return [s for s in steps if id(s) not in removed]
+
+
 def decode_attention_rows(itemsize: int) -> int:
     """Cache rows one pass of the decode-attention workgroup covers: 256
     threads, one 16-byte vector per lane, 64-element rows."""
@@ -1228,10 +1293,13 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
                                     tickets, partials)]
         return kind, ptrs, ints, [a["divisor"]]
     if kind == K_GEMM:
-        x, w = step.ins
+        x, w = step.ins[0], step.ins[1]
         out = step.outs[0]
-        return kind, [_ptr(x), _ptr(w), _ptr(out)], [
-            a["rows"], a["N"], a["K"], dtype_code(x.dtype), x.row_stride(), w.strides[0], a["N"]], []
+        res, up = a.get("res"), a.get("up")
+        return kind, [_ptr(x), _ptr(w), _ptr(out), _ptr(res), _ptr(up)], [
+            a["rows"], a["N"], a["K"], dtype_code(x.dtype), x.row_stride(), w.strides[0], a["N"],
+            a["N"] if res is not None else 0, 1 if up is not None else 0,
+            up.strides[0] if up is not None else 0, 1 if res is not None else 0], []
     if kind == K_GEMV:
         segments = a["segments"]
         prologue = a["prologue"]
@@ -1317,6 +1385,7 @@ def plan_graph(compiler, outputs: Sequence[LazyNode], dynamic_inputs: Sequence[L
     steps = fuse_rmsnorm_prologue(steps, out_pvs)
     steps = fuse_silu_gemv(steps, out_pvs)
     steps = fuse_residual(steps, out_pvs)
+    steps = fuse_gemm_epilogues(steps, out_pvs)
     steps = merge_sibling_gemvs(steps)
     steps = fuse_decode_attention(steps, out_pvs, emitter)
 

@@ -47,11 +47,23 @@ template <> struct Mfma<bf16_t> {
   }
 };
 
-// p[0] A, p[1] W, p[2] C.
-// n[0] M, n[1] N, n[2] K, n[3] dtype, n[4] lda, n[5] ldw, n[6] ldc (elements).
-template <typename T, int BM, int BN>
+// p[0] A, p[1] W (the gate weight with SILU), p[2] C, p[3] residual R (or
+// null), p[4] the up weight (SILU).
+// n[0] M, n[1] N, n[2] K, n[3] dtype, n[4] lda, n[5] ldw, n[6] ldc,
+// n[7] ldr, n[8] SiLU epilogue, n[9] ldw of the up weight, n[10] residual
+// epilogue (elements; the planner picks the kernel from these flags, the
+// pointers are bound later).
+// Epilogues (the portable graph's rounding points, as in the decode GEMVs):
+//  * RES:  C = round(R + round(acc))
+//  * SILU: the tile's weight rows alternate, 16 at a time, between the gate
+//    and the up matrix for the same output columns, so a lane holds g and u
+//    of one element: C = round(silu(round(g)) * round(u)) with
+//    silu(g) = round(g / round(round(exp(-g)) + 1)); the output tile is
+//    BN / 2 columns wide.
+template <typename T, int BM, int BN, bool SILU, bool RES>
 __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
   using E = Elem<T>;
+  constexpr int ON = SILU ? BN / 2 : BN;  // output columns per tile
   constexpr int TM = BM / 2 / 16, TN = BN / 2 / 16;        // 16x16 tiles per wave
   constexpr int AV = BM * kBK / 8 / 256, WV = BN * kBK / 8 / 256;  // 16-byte vectors per thread
   static_assert(AV >= 1 && WV >= 1, "tile too small for 256 threads");
@@ -63,13 +75,16 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
   const T* A = static_cast<const T*>(a.p[0]);
   const T* W = static_cast<const T*>(a.p[1]);
   T* C = static_cast<T*>(a.p[2]);
+  const T* R = static_cast<const T*>(a.p[3]);
+  const T* Wu = static_cast<const T*>(a.p[4]);
+  const int64_t ldr = a.n[7], ldwu = a.n[9];
 
-  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + ON - 1) / ON;
   const int64_t tiles = tiles_m * tiles_n;
   const int64_t per_xcd = (tiles + 7) / 8;
   const int64_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (tile >= tiles) return;  // whole block: no barrier is skipped by part of it
-  const int64_t m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+  const int64_t m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * ON;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -87,8 +102,16 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
 #pragma unroll
     for (int t = 0; t < WV; ++t) {
       const int v = tid + 256 * t, r = v >> 3, c = v & 7;
-      const int64_t n = n0 + r, k = k0 + c * 8;
-      rw[t] = (n < N && k < K) ? *reinterpret_cast<const uint4*>(W + n * ldw + k) : make_uint4(0, 0, 0, 0);
+      const int64_t k = k0 + c * 8;
+      if (SILU) {  // 16-row fragments alternate gate, up (same columns)
+        const int f = r >> 4;
+        const int64_t n = n0 + 16 * (f >> 1) + (r & 15);
+        const T* src = (f & 1) ? Wu + n * ldwu : W + n * ldw;
+        rw[t] = (n < N && k < K) ? *reinterpret_cast<const uint4*>(src + k) : make_uint4(0, 0, 0, 0);
+      } else {
+        const int64_t n = n0 + r;
+        rw[t] = (n < N && k < K) ? *reinterpret_cast<const uint4*>(W + n * ldw + k) : make_uint4(0, 0, 0, 0);
+      }
     }
   };
   auto store_stage = [&](int buf) {
@@ -136,6 +159,24 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
     buf ^= 1;
   }
 
+  if (SILU) {
+    // fragment wn * TN + j of the tile: even = gate, odd = up, same columns
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; j += 2) {
+        const int64_t n = n0 + 16 * ((wn * TN + j) >> 1) + fi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = m0 + wm * (BM / 2) + i * 16 + fg * 4 + r;
+          const float g = E::round(acc[i][j][r]);
+          const float u = E::round(acc[i][j + 1][r]);
+          const float denom = E::round(E::round(expf(-g)) + 1.f);
+          if (m < M && n < N) C[m * ldc + n] = E::from_f(E::round(E::round(g / denom) * u));
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -144,15 +185,25 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t m = m0 + wm * (BM / 2) + i * 16 + fg * 4 + r;
-        if (m < M && n < N) C[m * ldc + n] = E::from_f(acc[i][j][r]);
+        if (m < M && n < N) {
+          float y = E::round(acc[i][j][r]);
+          if (RES) y = E::round(E::to_f(R[m * ldr + n]) + y);
+          C[m * ldc + n] = E::from_f(y);
+        }
       }
     }
 }
 
+template <typename T, bool SILU, bool RES>
+const void* pick_gemm_tile(bool big) {
+  return big ? reinterpret_cast<const void*>(&k_gemm_nt<T, 128, 128, SILU, RES>)
+             : reinterpret_cast<const void*>(&k_gemm_nt<T, 64, 64, SILU, RES>);
+}
+
 template <typename T>
-const void* pick_gemm(bool big) {
-  return big ? reinterpret_cast<const void*>(&k_gemm_nt<T, 128, 128>)
-             : reinterpret_cast<const void*>(&k_gemm_nt<T, 64, 64>);
+const void* pick_gemm(bool big, bool silu, bool res) {
+  if (silu) return pick_gemm_tile<T, true, false>(big);
+  return res ? pick_gemm_tile<T, false, true>(big) : pick_gemm_tile<T, false, false>(big);
 }
 
 const char* plan_gemm(KArgs& a, Launch& l) {
@@ -162,14 +213,19 @@ const char* plan_gemm(KArgs& a, Launch& l) {
   if (dt != F16 && dt != BF16) return "gemm: float16 or bfloat16 operands required";
   if (K % 8 || a.n[4] % 8 || a.n[5] % 8) return "gemm: k and row strides must be multiples of 8 elements";
   if (a.n[4] < K || a.n[5] < K || a.n[6] < N) return "gemm: row stride shorter than the row";
-  // 128 x 128 tiles once they fill the chip twice over, else 64 x 64
-  const int64_t big_tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  const bool silu = a.n[8] != 0, res = a.n[10] != 0;
+  if (silu && (res || a.n[9] % 8 || a.n[9] < K)) return "gemm: bad SiLU operands";
+  if (res && a.n[7] < N) return "gemm: residual row stride shorter than the row";
+  // 128 x 128 tiles once they fill the chip twice over, else 64 x 64 (output
+  // tiles are half as wide with the SiLU pair)
+  const int64_t span = silu ? 2 : 1;
+  const int64_t big_tiles = ((M + 127) / 128) * ((N * span + 127) / 128);
   const bool big = big_tiles >= 512;
-  const int64_t bm = big ? 128 : 64;
-  const int64_t tiles = ((M + bm - 1) / bm) * ((N + bm - 1) / bm);
+  const int64_t bm = big ? 128 : 64, on = bm / span;
+  const int64_t tiles = ((M + bm - 1) / bm) * ((N + on - 1) / on);
   const int64_t blocks = 8 * ((tiles + 7) / 8);
   if (blocks > 2147483647) return "gemm: too many tiles";
-  l.func = dt == F16 ? pick_gemm<__half>(big) : pick_gemm<bf16_t>(big);
+  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res) : pick_gemm<bf16_t>(big, silu, res);
   l.grid = dim3(static_cast<unsigned>(blocks));
   l.block = dim3(256);
   l.shmem = 0;

@@ -422,10 +422,19 @@ def s_gemv(mem, p, n, f):
 
 
 def s_gemm(mem, p, n, f):
-    M, N, K, dt, lda, ldw, ldc = n[0:7]
+    M, N, K, dt, lda, ldw, ldc, ldr, silu, ldwu, has_res = n[0:11]
     A = load(mem, p[0], dt, np.arange(M)[:, None] * lda + np.arange(K)[None, :])
     W = load(mem, p[1], dt, np.arange(N)[:, None] * ldw + np.arange(K)[None, :])
     C = _round((A.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32), dt)
+    if silu:  # C = round(silu(round(g)) * round(u)), silu(g) = round(g / round(round(exp(-g)) + 1))
+        Wu = load(mem, p[4], dt, np.arange(N)[:, None] * ldwu + np.arange(K)[None, :])
+        U = _round((A.astype(np.float64) @ Wu.T.astype(np.float64)).astype(np.float32), dt)
+        with np.errstate(over="ignore"):
+            denom = _round(_round(np.exp(-C), dt) + 1, dt)
+        C = _round(_round(C / denom, dt) * U, dt)
+    elif has_res:  # residual epilogue
+        R = load(mem, p[3], dt, np.arange(M)[:, None] * ldr + np.arange(N)[None, :])
+        C = _round(R + C, dt)
     store(mem, p[2], dt, (np.arange(M)[:, None] * ldc + np.arange(N)[None, :]).reshape(-1), C.reshape(-1))
     return 0
 

@@ -260,3 +260,31 @@ def test_safetensors_loading(hip, tmp_path):
     bf = load_safetensors(path, hip.device, dtype=BFLOAT16)
     np.testing.assert_array_equal(bf["b"].numpy(compiler="hip").view(np.uint16),
                                   to_bf16(np.ones(4, np.float32)).view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("S", [12, 200])
+def test_prefill_gemm_epilogues_match_oracle(hip, dtype, S):
+    """A 16-bit prefill layer through the MFMA GEMM with its fused epilogues:
+    gate/up as one GEMM with the SiLU product, o_proj and down_proj adding
+    the residual (FFN width 688 leaves ragged output tiles)."""
+    from chomikgrad import synthetic
+    from chomikgrad._planner import K_ELEMENTWISE, K_GEMM
+    from chomikgrad.llama import LlamaConfig, LlamaForCausalLM, position_selector
+
+    announce(f"prefill GEMM epilogues {dtype_name(dtype)} S={S}")
+    config = LlamaConfig(vocab_size=128, hidden_size=256, intermediate_size=688, num_hidden_layers=1,
+                         num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=256)
+    weights = synthetic.weights_as_tensors(synthetic.host_weights(config, dtype, seed=11))
+    model = LlamaForCausalLM(config, weights, sequence_length=S, cache_length=S, dtype=dtype)
+    tokens = Tensor(np.random.default_rng(S).integers(0, 128, (1, S)).astype(np.int32), copy=False)
+    outputs = model.prefill(tokens, Tensor(position_selector(S - 1, S, dtype=dtype)))
+    program = compile_graph(*outputs, compiler="hip", dynamic_inputs=(tokens,))
+    gemms = [s for s in program._planned.steps if s.kind == K_GEMM]
+    assert sum(g.attrs.get("up") is not None for g in gemms) == 1
+    assert sum(g.attrs.get("res") is not None for g in gemms) == 2
+    assert not any(s.kind == K_ELEMENTWISE for s in program._planned.steps)
+    got = program()
+    expected = realize(*outputs, compiler="cpu")
+    for value, reference in zip(got, expected):
+        np.testing.assert_allclose(as_float(value), as_float(reference), rtol=2e-2, atol=3e-2)

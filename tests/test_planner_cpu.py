@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from chomikgrad import Tensor, realize, synthetic
-from chomikgrad._planner import (K_DECODE_ATTN, K_FILL, K_GEMM, K_GEMV, K_KV_PLACE, K_KV_WRITE, K_MATMUL,
+from chomikgrad._planner import (K_DECODE_ATTN, K_ELEMENTWISE, K_FILL, K_GEMM, K_GEMV, K_KV_PLACE, K_KV_WRITE, K_MATMUL,
                                  K_SDPA, plan_graph)
 from chomikgrad.dtypes import BFLOAT16, bf16_to_float32, to_bf16
 from chomikgrad.llama import (
@@ -176,7 +176,10 @@ def test_half_precision_prefill_uses_mfma_gemm(dtype):
     expected = realize(*outputs, compiler="cpu")
     planned, got = model_run(outputs, [tokens])
     gemms = [s for s in planned.steps if s.kind == K_GEMM]
-    assert len(gemms) == 7  # q, k, v, o, gate, up, down
+    assert len(gemms) == 6  # q, k, v, o (+ residual), gate/up (+ SiLU), down (+ residual)
+    assert sum(g.attrs.get("up") is not None for g in gemms) == 1
+    assert sum(g.attrs.get("res") is not None for g in gemms) == 2
+    assert not any(s.kind == K_ELEMENTWISE for s in planned.steps)
     # the cache placements K^T @ eye(S, C) become fill + strided copy; the one
     # generic matmul left is the last-row selector
     assert sum(s.kind == K_FILL for s in planned.steps) == 2

@@ -133,6 +133,193 @@ class LlamaRuntime:
         self._decoder_programs[key] = entry
         return entry
 
+    # -- verification block (speculative decoding) -------------------------------------
+    def _verifier(self, block: int, context: int, position: int, caches: List[Any]):
+        """Compile (once per (block, context)) the target's verification block:
+        ``block`` tokens at ``position`` against the caches, returning their
+        logits (1, block, V) and the caches with the block written
+        (generate_tinyllama.py:396-488, LlamaDecoderBlock).  Caches are
+        donated: the block updates them in place."""
+        key = (block, context)
+        cached = self._block_programs.get(key)
+        if cached is not None:
+            return cached
+        c = self.config
+        placement, write, attention = block_masks(position, block, context, self.dtype)
+        leaves = [
+            Tensor(np.zeros((1, block), dtype=np.int32), copy=False),
+            Tensor(_rope_rotations(block, c.head_size, c.rope_theta, self.dtype, offset=position), copy=False),
+            Tensor(attention, copy=False),
+            Tensor(placement, copy=False),
+            Tensor(write, copy=False),
+            Tensor(np.asarray(position, dtype=np.int32), copy=False),
+        ]
+        cache_tensors = [
+            Tensor.from_native(value, backend=self.device.name, shape=tuple(value.shape), dtype=self.dtype)
+            for value in caches
+        ]
+        decoder = LlamaDecoderBlock(c, self.weights, block_length=block, cache_length=context, dtype=self.dtype)
+        outputs = decoder(*leaves[:5], list(zip(cache_tensors[::2], cache_tensors[1::2])), position=leaves[5])
+        dynamic = leaves + cache_tensors
+        kwargs = {"donate": [t._node for t in cache_tensors]} if self.compiler_name == "hip" else {}
+        program = self.compiler.compile([o._node for o in outputs], [t._node for t in dynamic], **kwargs)
+        entry = (program, [t._node for t in dynamic])
+        self._block_programs[key] = entry
+        return entry
+
+    def _decode_step(self, token: int, position: int, context: int, caches: List[Any]):
+        """One decode step with host-built rotation and masks (the reference's
+        _run_decoder_step, generate_tinyllama.py:309-393): returns (logits,
+        caches)."""
+        c = self.config
+        donate = self.compiler_name == "hip"
+        program, nodes = self._decoder(context, position, caches, donate=donate)
+        attention, write = decode_masks(position, context, self.dtype)
+        values = [
+            self.device.array(np.asarray([[token]], dtype=np.int32)),
+            self.device.array(_rope_rotations(1, c.head_size, c.rope_theta, self.dtype, offset=position)),
+            self.device.array(attention),
+            self.device.array(write),
+            self.device.array(np.asarray(position, dtype=np.int32)),
+            *caches,
+        ]
+        native = program.run(dict(zip(nodes, values)), synchronize=False)
+        return native[0], list(native[1:])
+
+    def _verify_block(self, inputs: Sequence[int], position: int, context: int, caches: List[Any]):
+        """Run the verification block over ``inputs`` at ``position``: returns
+        the target's greedy prediction after each input and the caches."""
+        c = self.config
+        block = len(inputs)
+        program, nodes = self._verifier(block, context, position, caches)
+        placement, write, attention = block_masks(position, block, context, self.dtype)
+        values = [
+            self.device.array(np.asarray([inputs], dtype=np.int32)),
+            self.device.array(_rope_rotations(block, c.head_size, c.rope_theta, self.dtype, offset=position)),
+            self.device.array(attention),
+            self.device.array(placement),
+            self.device.array(write),
+            self.device.array(np.asarray(position, dtype=np.int32)),
+            *caches,
+        ]
+        native = program.run(dict(zip(nodes, values)), synchronize=False)
+        predictions = np.asarray(self.device.argmax_last_axis(native[0])).reshape(-1)
+        return [int(t) for t in predictions], list(native[1:])
+
+    def generate_speculative(
+        self,
+        draft: "LlamaRuntime",
+        prompt: Sequence[int],
+        max_new_tokens: int,
+        *,
+        speculative_tokens: int = 4,
+        draft_prompt: Optional[Sequence[int]] = None,
+        bonus: bool = False,
+        stop_at_eos: bool = False,
+    ) -> Dict[str, object]:
+        """Greedy speculative decoding with ``draft`` proposing for this
+        (target) runtime -- the reference's _generate_speculative_loaded
+        (generate_tinyllama.py:491-622):
+
+        * the first token comes from the target's prefill; the draft prefills
+          its own prompt (``draft_prompt``, default the same ids);
+        * each round the draft proposes up to ``speculative_tokens`` greedy
+          tokens, one decode step each, starting from the last emitted token;
+        * the target verifies them in one block and the longest agreeing
+          prefix plus the target's own next token is emitted
+          (verify_greedy_candidates, generation.py:15-28).
+
+        ``bonus=False`` is the reference's block ``[last, d1 .. d_{k-1}]``
+        (k predictions, no extra token when all k agree).  ``bonus=True``
+        verifies ``[last, d1 .. dk]`` (k + 1 predictions): when all k agree
+        the target's prediction after ``dk`` is emitted as well, and the
+        draft, which never consumed ``dk``, catches up with one extra step
+        before its next proposal.  Either way the emitted sequence equals the
+        target's own greedy decoding."""
+        from .generation import verify_greedy_candidates
+
+        if max_new_tokens <= 0:
+            raise ValueError("max_new_tokens must be positive")
+        if speculative_tokens <= 0:
+            raise ValueError("speculative_tokens must be positive")
+        if not len(prompt):
+            raise ValueError("the prompt produced no tokens")
+        draft_prompt = list(prompt) if draft_prompt is None else list(draft_prompt)
+        context = len(prompt) + max_new_tokens + (1 if bonus else 0)
+        draft_context = len(draft_prompt) + max_new_tokens + 1
+        for runtime, length in ((self, context), (draft, draft_context)):
+            if length > runtime.config.max_position_embeddings:
+                raise ValueError(f"prompt plus output is {length} tokens, model limit is "
+                                 f"{runtime.config.max_position_embeddings}")
+        eos = self.config.eos_token_id
+        started = time.perf_counter()
+        with no_grad():
+            logits, target_caches = self.prefill(prompt, context)
+            token = self.device.argmax(logits)
+            first_token_seconds = time.perf_counter() - started
+            _, draft_caches = draft.prefill(draft_prompt, draft_context)
+            generated = [token]
+            tokens = list(prompt) + [token]
+            decode_started = time.perf_counter()
+            accepted = proposed = verifications = draft_calls = 0
+            lagging: Optional[int] = None  # a token the draft has not consumed yet
+            while len(generated) < max_new_tokens and not (stop_at_eos and token == eos):
+                limit = min(speculative_tokens, max_new_tokens - len(generated))
+                draft_position = len(draft_prompt) + len(generated) - 1
+                if lagging is not None:  # consume dk before proposing from the bonus token
+                    _, draft_caches = draft._decode_step(lagging, draft_position - 1, draft_context, draft_caches)
+                    draft_calls += 1
+                    lagging = None
+                proposal: List[int] = []
+                draft_token = token
+                for _ in range(limit):
+                    draft_logits, draft_caches = draft._decode_step(draft_token, draft_position, draft_context,
+                                                                    draft_caches)
+                    draft_token = draft.device.argmax(draft_logits)
+                    proposal.append(draft_token)
+                    draft_calls += 1
+                    draft_position += 1
+                    if stop_at_eos and draft_token == eos:
+                        break
+                block = [token, *proposal] if bonus else [token, *proposal[:-1]]
+                predictions, target_caches = self._verify_block(block, len(tokens) - 1, context, target_caches)
+                if bonus:
+                    decision = verify_greedy_block_with_bonus(proposal, predictions)
+                    if decision.accepted_draft_tokens == len(proposal):
+                        lagging = proposal[-1]
+                else:
+                    decision = verify_greedy_candidates(proposal, predictions)
+                emitted = list(decision.emitted_tokens)[: max_new_tokens - len(generated)]
+                if stop_at_eos and eos in emitted:
+                    emitted = emitted[: emitted.index(eos) + 1]
+                tokens.extend(emitted)
+                generated.extend(emitted)
+                token = emitted[-1]
+                accepted += decision.accepted_draft_tokens
+                proposed += len(proposal)
+                verifications += 1
+            self.device.synchronize()
+        decode_seconds = time.perf_counter() - decode_started
+        decode_tokens = len(generated) - 1
+        return {
+            "loop": "speculative" + ("-bonus" if bonus else ""),
+            "generated_token_ids": generated,
+            "prompt_tokens": len(prompt),
+            "generated_tokens": len(generated),
+            "first_token_seconds": first_token_seconds,
+            "decode_seconds": decode_seconds,
+            "warm_tokens_per_second": decode_tokens / decode_seconds if decode_tokens else None,
+            "wall_generation_seconds": time.perf_counter() - started,
+            "fixed_context_tokens": context,
+            "speculative_tokens": speculative_tokens,
+            "accepted_draft_tokens": accepted,
+            "proposed_draft_tokens": proposed,
+            "acceptance_rate": accepted / proposed if proposed else 0.0,
+            "target_verification_calls": verifications,
+            "draft_decode_calls": draft_calls,
+            "kv_cache": True,
+        }
+
     # -- generation ------------------------------------------------------------------
     def generate(
         self,

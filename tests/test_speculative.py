@@ -1,0 +1,120 @@
+"""Greedy speculative decoding (the reference's _generate_speculative_loaded,
+examples/generate_tinyllama.py:491-622): the emitted sequence must equal the
+target's own greedy decoding whatever the draft proposes
+(tinyllama_speculative.py:123 in the reference checks exactly that).  The
+driver is compiler-agnostic, so these CPU tests run it on the oracle; the
+GPU tests repeat it on the hip plugin and at the C5 shapes."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from chomikgrad import synthetic
+from chomikgrad.llama import LlamaConfig
+from chomikgrad.runtime import LlamaRuntime
+
+
+def tiny_pair(dtype=np.float32):
+    target_cfg = LlamaConfig(vocab_size=96, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                             num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=128)
+    draft_cfg = LlamaConfig(vocab_size=96, hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                            num_attention_heads=2, num_key_value_heads=1, max_position_embeddings=128)
+    target = synthetic.weights_as_tensors(synthetic.host_weights(target_cfg, dtype, seed=5))
+    draft = synthetic.weights_as_tensors(synthetic.host_weights(draft_cfg, dtype, seed=6))
+    return target_cfg, target, draft_cfg, draft
+
+
+@pytest.mark.parametrize("bonus", [False, True], ids=["reference-block", "bonus-block"])
+@pytest.mark.parametrize("k", [1, 3])
+def test_speculative_equals_greedy_on_oracle(bonus, k):
+    target_cfg, target_w, draft_cfg, draft_w = tiny_pair()
+    target = LlamaRuntime(target_cfg, target_w, compiler="cpu", dtype=np.float32)
+    prompt = [5, 17, 3, 60, 2, 44]
+    greedy = target.generate(prompt, 12, loop="reference")["generated_token_ids"]
+    for draft_cfg_, draft_w_ in ((draft_cfg, draft_w), (target_cfg, target_w)):
+        draft = LlamaRuntime(draft_cfg_, draft_w_, compiler="cpu", dtype=np.float32)
+        result = target.generate_speculative(draft, prompt, 12, speculative_tokens=k, bonus=bonus)
+        assert result["generated_token_ids"] == greedy
+        assert result["proposed_draft_tokens"] >= result["accepted_draft_tokens"] >= 0
+    # the target drafting for itself accepts every proposal
+    assert result["acceptance_rate"] == 1.0
+    rounds = result["target_verification_calls"]
+    assert rounds == (-(-11 // (k + 1)) if bonus else -(-11 // k))
+
+
+def test_speculative_argument_checks():
+    target_cfg, target_w, draft_cfg, draft_w = tiny_pair()
+    target = LlamaRuntime(target_cfg, target_w, compiler="cpu", dtype=np.float32)
+    draft = LlamaRuntime(draft_cfg, draft_w, compiler="cpu", dtype=np.float32)
+    with pytest.raises(ValueError):
+        target.generate_speculative(draft, [1, 2], 0)
+    with pytest.raises(ValueError):
+        target.generate_speculative(draft, [1, 2], 4, speculative_tokens=0)
+    with pytest.raises(ValueError):
+        target.generate_speculative(draft, [], 4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bonus", [False, True], ids=["reference-block", "bonus-block"])
+def test_speculative_on_hip_matches_oracle_and_greedy(hip, bonus):
+    print(f"[gpu case] speculative tiny bonus={bonus}", flush=True)
+    target_cfg, target_w, draft_cfg, draft_w = tiny_pair()
+    prompt = [5, 17, 3, 60, 2, 44]
+    oracle = LlamaRuntime(target_cfg, target_w, compiler="cpu", dtype=np.float32).generate_speculative(
+        LlamaRuntime(draft_cfg, draft_w, compiler="cpu", dtype=np.float32), prompt, 12, speculative_tokens=3,
+        bonus=bonus)
+    target = LlamaRuntime(target_cfg, target_w, compiler="hip", dtype=np.float32)
+    draft = LlamaRuntime(draft_cfg, draft_w, compiler="hip", dtype=np.float32)
+    got = target.generate_speculative(draft, prompt, 12, speculative_tokens=3, bonus=bonus)
+    assert got["generated_token_ids"] == oracle["generated_token_ids"]
+    assert got["accepted_draft_tokens"] == oracle["accepted_draft_tokens"]
+    assert got["generated_token_ids"] == target.generate(prompt, 12, loop="resident")["generated_token_ids"]
+
+
+@pytest.mark.gpu
+def test_c5_speculative_full_shape_equals_greedy(hip):
+    """C5: 2-layer dim-512 fp16 draft proposing k = 4 for the TinyLlama-shape
+    fp16 target, 5-token verification blocks, 256-token random prompt, 256
+    tokens.  The verification block (multi-row GEMV, generic attention) and
+    the single-token decode step compute in different orders, and the top two
+    logits of a random-init model are often within float16 noise, so the two
+    runs may part at such a near-tie.  Checked: the first 32 tokens agree
+    (the decode parity bar), and at the first divergence, if any, the
+    speculative token is greedy decoding's runner-up with a margin within
+    float16 noise -- a driver error (a wrong position, a stale cache row)
+    would pick neither."""
+    print("[gpu case] C5 speculative, full shape", flush=True)
+    target_spec, draft_spec = synthetic.TINYLLAMA, synthetic.DRAFT
+    target = LlamaRuntime(target_spec.config, synthetic.weights_as_tensors(
+        synthetic.host_weights(target_spec.config, target_spec.dtype, seed=0)), compiler="hip", dtype=target_spec.dtype)
+    draft = LlamaRuntime(draft_spec.config, synthetic.weights_as_tensors(
+        synthetic.host_weights(draft_spec.config, draft_spec.dtype, seed=1)), compiler="hip", dtype=draft_spec.dtype)
+    prompt = synthetic.prompt_ids(target_spec.config.vocab_size, 256, seed=0).tolist()
+    result = target.generate_speculative(draft, prompt, 256, speculative_tokens=4, bonus=True)
+    assert result["generated_tokens"] == 256
+    # plain greedy decoding, recording every step's logits
+    rows = []
+    device = target.device
+    original = device.argmax
+
+    def record(value):
+        rows.append(np.asarray(device.to_numpy(value), dtype=np.float32).reshape(-1))
+        return original(value)
+
+    device.argmax = record
+    try:
+        greedy = target.generate(prompt, 256, loop="reference")["generated_token_ids"]
+    finally:
+        device.argmax = original
+    spec = result["generated_token_ids"]
+    assert spec[:32] == greedy[:32]
+    diverged = next((i for i, (a, b) in enumerate(zip(spec, greedy)) if a != b), None)
+    if diverged is not None:
+        logits = rows[diverged]
+        order = np.argsort(-logits, kind="stable")
+        assert spec[diverged] == int(order[1]), "speculative token is not greedy's runner-up"
+        margin = float(logits[order[0]] - logits[order[1]])
+        assert margin <= 0.02, f"divergence at a margin of {margin}"
+    print(f"C5: {result['warm_tokens_per_second']:.1f} tok/s, acceptance {result['acceptance_rate']:.3f}, "
+          f"{result['target_verification_calls']} verification blocks, first divergence {diverged}", flush=True)

@@ -9,6 +9,12 @@ synchronisation.  Decoding uses the device-resident greedy loop (the KV
 caches are donated and updated in place; token, position and masks advance
 on the device; no host round trip per token).
 
+Further fields: ``prefill_c3`` (the 2048-token C3 prefill with MFMA
+utilisation and a per-kernel breakdown), ``c4_batched_decode`` (C4, 8 bf16
+sequences over 4096 filled cache rows, device-resident loop) and
+``c5_speculative`` (C5, draft + 5-token verification blocks) -- reported
+alongside, not the headline metric.
+
 Besides the JSON line's ``value`` (decode tok/s), ``roofline`` describes the
 dominant kernel (the largest share of decode time per token) from HIP-event
 timings of the real decode plan's launches, with the HBM traffic per launch
@@ -64,7 +70,7 @@ def kernel_label(step) -> str:
 def algorithmic_bytes(step) -> int:
     """Bytes a kernel must move at minimum: every operand read once, every
     result written once (KV writes in place touch one row per head)."""
-    from chomikgrad._planner import K_GATHER, K_GEMV, K_KV_WRITE
+    from chomikgrad._planner import K_DECODE_ATTN, K_GATHER, K_GEMV, K_KV_WRITE
 
     if step.kind == K_GATHER:
         # the gathered rows (read once, written once) and the indices
@@ -74,6 +80,17 @@ def algorithmic_bytes(step) -> int:
     if step.kind == K_GEMV:
         total = sum(pv.size * pv.itemsize for pv in step.reads())
         return total + sum(pv.size * pv.itemsize for pv in {id(o.storage): o for o in step.outs}.values())
+    if step.kind == K_DECODE_ATTN:
+        # q, k, v, the position, one RoPE table row, both caches and both
+        # masks read once; the output and (in place) one written row per KV
+        # head and cache -- the combine scratch and tickets are not operands
+        q, k, v, position, table, cache_k, cache_v, w, mask, _tickets, _partials = step.ins
+        reads = sum(pv.size * pv.itemsize for pv in (q, k, v, position, cache_k, cache_v, w, mask))
+        reads += table.shape[1] * table.itemsize
+        out = step.outs[0]
+        rows = cache_k.shape[0] * cache_k.shape[1] * cache_k.shape[3] * cache_k.itemsize
+        written = 2 * rows if step.attrs.get("in_place") else 2 * cache_k.size * cache_k.itemsize
+        return reads + out.size * out.itemsize + written
     if step.kind == K_KV_WRITE and step.attrs.get("in_place"):
         cache, x, w = step.ins
         row = cache.shape[0] * cache.shape[1] * cache.shape[3] * cache.itemsize
@@ -201,6 +218,116 @@ def prefill_measurement(runtime, config, device, lib, tokens: int, runs: int) ->
     }
 
 
+def c4_measurement(device, lib, steps: int, warmup: int) -> dict:
+    """C4: Llama-3.2-1B-shape bf16 (tied embedding/LM head, RoPE theta 5e5),
+    8 sequences decoding greedily together over per-sequence caches whose
+    first 4096 rows are filled (synthetic rows, the same block for every
+    layer) -- the device-resident batched loop, ``steps`` timed steps."""
+    from chomikgrad import Tensor, synthetic
+    from chomikgrad.dtypes import as_dtype
+    from chomikgrad.llama import LlamaBatchedDecoderStep, _rope_rotations, decode_masks
+
+    spec = synthetic.LLAMA32_1B
+    cfg, dtype = spec.config, spec.dtype
+    batch, filled = 8, 4096
+    context = filled + 1 + warmup + steps
+    started = time.perf_counter()
+    weights = synthetic.weights_as_tensors(synthetic.host_weights(cfg, dtype, seed=0, tie_embeddings=True))
+    rng = np.random.default_rng(7)
+    block = np.zeros((batch, cfg.num_key_value_heads, context, cfg.head_size), np.float32)
+    block[:, :, :filled] = rng.standard_normal((batch, cfg.num_key_value_heads, filled, cfg.head_size),
+                                               dtype=np.float32) * 0.5
+    block = as_dtype(block, dtype)
+    caches = [device.array(block) for _ in range(2 * cfg.num_hidden_layers)]
+    log(f"C4 weights and caches ready in {time.perf_counter() - started:.1f} s")
+    positions = np.full(batch, filled, np.int32)
+    attention = np.concatenate([decode_masks(filled, context, np.float32)[0]] * batch).reshape(batch, 1, 1, context)
+    write = np.concatenate([decode_masks(filled, context, np.float32)[1]] * batch).reshape(batch, 1, context, 1)
+    rotation = np.concatenate([_rope_rotations(1, 64, cfg.rope_theta, np.float32, offset=filled)] * batch)
+    leaves = [Tensor(np.zeros((batch, 1), np.int32), copy=False),
+              Tensor(as_dtype(rotation.reshape(batch, 1, 1, 64, 64), dtype), copy=False),
+              Tensor(as_dtype(attention, dtype), copy=False), Tensor(as_dtype(write, dtype), copy=False),
+              Tensor(positions, copy=False)]
+    cache_tensors = [Tensor.from_native(c, backend=device.name, shape=tuple(c.shape), dtype=dtype) for c in caches]
+    step = LlamaBatchedDecoderStep(cfg, weights, batch=batch, cache_length=context, dtype=dtype)
+    outputs = step(*leaves[:4], list(zip(cache_tensors[::2], cache_tensors[1::2])), position=leaves[4])
+    from chomikgrad import get_compiler
+    hip = get_compiler("hip")
+    program = hip.compile([o._node for o in outputs], [t._node for t in leaves + cache_tensors],
+                          donate=[t._node for t in cache_tensors])
+    if leaves[1]._node in program.inputs:
+        raise RuntimeError("the C4 program does not lower RoPE")
+    tokens = device.array(np.random.default_rng(8).integers(0, cfg.vocab_size, (batch, 1)).astype(np.int32))
+    position = device.array(positions)
+    attention_d = device.array(as_dtype(attention, dtype))
+    write_d = device.array(as_dtype(write, dtype))
+    bindings = dict(zip([t._node for t in leaves + cache_tensors],
+                        [tokens, device.array(as_dtype(rotation.reshape(batch, 1, 1, 64, 64), dtype)),
+                         attention_d, write_d, position, *caches]))
+    logits = device.empty((batch, cfg.vocab_size), dtype)
+
+    def run(count):
+        for _ in range(count):
+            program.run(bindings, out=[logits])
+            device.greedy_advance(logits, tokens, position=position, attention_mask=attention_d,
+                                  write_mask=write_d, cache_length=context)
+
+    run(warmup)
+    device.synchronize()
+    start, stop = ctypes.c_void_p(), ctypes.c_void_p()
+    lib.call("chip_event_create", ctypes.byref(start))
+    lib.call("chip_event_create", ctypes.byref(stop))
+    lib.call("chip_event_record", start)
+    run(steps)
+    lib.call("chip_event_record", stop)
+    device.synchronize()
+    ms = ctypes.c_float(0.0)
+    lib.call("chip_event_elapsed_ms", start, stop, ctypes.byref(ms))
+    lib.call("chip_event_destroy", start)
+    lib.call("chip_event_destroy", stop)
+    seconds = ms.value * 1e-3
+    first = filled + warmup
+    kv_per_position = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_size * 2
+    weight_bytes = weights_bytes(cfg, 2) + (batch - 1) * cfg.hidden_size * 2  # one embedding row per sequence
+    kv_bytes = batch * kv_per_position * float(np.mean(np.arange(first, first + steps) + 2))  # read p + 1, write 1
+    per_step = weight_bytes + kv_bytes
+    return {
+        "workload": "C4: Llama-3.2-1B-shape bf16, batch 8 greedy decode over 4096 filled cache positions",
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms.value / steps, 4),
+        "tok_per_s": round(batch * steps / seconds, 1),
+        "bytes_per_step": int(per_step), "achieved_gbps": round(per_step * steps / seconds / 1e9, 1),
+        "roofline_frac": round(per_step * steps / seconds / 1e9 / HBM_PEAK_GBPS, 4),
+        "program_kernels": program.kernel_count + 1,
+        "kernel_breakdown": plan_breakdown(program, lib, rounds=3),
+    }
+
+
+def c5_measurement(target, tokens: int) -> dict:
+    """C5: the 2-layer dim-512 fp16 draft (seed 1) proposing k = 4 greedy
+    tokens per round for the C2 target, verified in 5-token blocks; 256-token
+    random prompt.  Timed on the second (warm) run."""
+    from chomikgrad import synthetic
+    from chomikgrad.runtime import LlamaRuntime
+
+    spec = synthetic.DRAFT
+    draft = LlamaRuntime(spec.config, synthetic.weights_as_tensors(synthetic.host_weights(spec.config, spec.dtype, seed=1)),
+                         compiler="hip", dtype=spec.dtype)
+    prompt = synthetic.prompt_ids(target.config.vocab_size, 256, seed=0).tolist()
+    target.generate_speculative(draft, prompt, tokens, speculative_tokens=4, bonus=True)
+    result = target.generate_speculative(draft, prompt, tokens, speculative_tokens=4, bonus=True)
+    return {
+        "workload": "C5: greedy speculative decoding, 2-layer dim-512 draft (k = 4) for the C2 target, "
+                    "5-token verification blocks, 256-token prompt",
+        "generated_tokens": result["generated_tokens"],
+        "tok_per_s": round(result["warm_tokens_per_second"], 1),
+        "acceptance_rate": round(result["acceptance_rate"], 4),
+        "verification_blocks": result["target_verification_calls"],
+        "draft_steps": result["draft_decode_calls"],
+        "note": "independent random-init draft and target: acceptance is near 0, so each round emits the target's "
+                "own token after k draft steps",
+    }
+
+
 def cpu_baseline(config, weights, dtype, context: int, first_position: int, steps: int) -> dict:
     """Oracle decode steps on the host: the reference's NumPy cpu-plugin
     algorithm, float16, with zero-filled caches of the real context length.
@@ -255,6 +382,8 @@ def main() -> int:
     parser.add_argument("--prefill-tokens", type=int, default=2048, help="C3 prefill length (0 skips it)")
     parser.add_argument("--prefill-runs", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--c4-steps", type=int, default=64, help="C4 batched decode steps (0 skips it)")
+    parser.add_argument("--c5-tokens", type=int, default=256, help="C5 speculative tokens (0 skips it)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs every kernel on a single MI355X and has no "
@@ -391,6 +520,17 @@ def main() -> int:
         prefill_c3 = prefill_measurement(runtime, config, device, lib, args.prefill_tokens, args.prefill_runs)
         log(f"C3 prefill: {prefill_c3['ms']} ms, {prefill_c3['achieved_tflops']} TFLOP/s")
 
+    c5 = None
+    if args.c5_tokens:
+        log(f"C5 speculative decoding of {args.c5_tokens} tokens")
+        c5 = c5_measurement(runtime, args.c5_tokens)
+        log(f"C5: {c5['tok_per_s']} tok/s, acceptance {c5['acceptance_rate']}")
+    c4 = None
+    if args.c4_steps:
+        log(f"C4 batched bf16 decode, {args.c4_steps} steps")
+        c4 = c4_measurement(device, lib, args.c4_steps, 4)
+        log(f"C4: {c4['tok_per_s']} tok/s, roofline {c4['roofline_frac']}")
+
     baseline = None
     if not args.no_cpu_baseline:
         log("timing the NumPy oracle on the host (bounded sample)")
@@ -426,6 +566,8 @@ def main() -> int:
         "gpu_event_ms_per_step": round(gpu_ms.value / args.steps, 4),
         "prefill_tok_per_s": round(PROMPT / prefill_seconds, 1),
         "prefill_c3": prefill_c3,
+        "c4_batched_decode": c4,
+        "c5_speculative": c5,
         "kernel_breakdown": breakdown,
         "first_tokens": tokens[:16],
     }

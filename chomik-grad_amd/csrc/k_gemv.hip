@@ -933,6 +933,158 @@ const void* pick_rows(int64_t m, int64_t kv, bool pro, bool silu, bool stage) {
   return pick<T, kMaxRows, 2, 8, 1>(pro, silu, stage);
 }
 
+// Few-row GEMV on MFMA (2 <= M <= 16 input rows, 16-bit types, no RMSNorm
+// prologue: the planner leaves that to k_rmsnorm for these shapes).  With M
+// rows every weight element feeds M products, which a VALU kernel cannot
+// keep up with at HBM speed; here each wave computes a 16-column output tile
+// for all rows with v_mfma_f32_16x16x32 (x rows padded to 16 as the A
+// operand, 16 weight rows as the B operand, both k-contiguous 16-byte loads
+// straight from memory).  Chunks of kChunk k-steps are double-buffered in
+// registers with unconditional (clamped) loads so the waits stay exact.  KS
+// waves of a block split K for one tile and add their partial tiles through
+// LDS.  Epilogues as k_gemv: residual, or the SiLU pair (the gate and up
+// rows of the same columns are two B operands).  Same KArgs layout as k_gemv.
+typedef _Float16 mh8v __attribute__((ext_vector_type(8)));
+typedef __bf16 mb8v __attribute__((ext_vector_type(8)));
+typedef float mf4v __attribute__((ext_vector_type(4)));
+template <typename T> struct SkinnyMfma;
+template <> struct SkinnyMfma<__half> {
+  __device__ static __forceinline__ mf4v step(const uint4& a, const uint4& b, mf4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8v, a), __builtin_bit_cast(mh8v, b), c, 0, 0, 0);
+  }
+};
+template <> struct SkinnyMfma<bf16_t> {
+  __device__ static __forceinline__ mf4v step(const uint4& a, const uint4& b, mf4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mb8v, a), __builtin_bit_cast(mb8v, b), c, 0, 0, 0);
+  }
+};
+
+constexpr int kChunk = 4;  // k-steps of 32 per register buffer
+
+template <typename T, int KS, bool SILU>
+__global__ __launch_bounds__(256) void k_gemv_mfma(KArgs a) {
+  using E = Elem<T>;
+  using F = SkinnyMfma<T>;
+  constexpr int TPB = 4 / KS;        // column tiles per block
+  constexpr int NB = SILU ? 2 : 1;   // B operands (gate, up)
+  __shared__ mf4v red[SILU ? 2 : 1][4][64];
+
+  const int M = static_cast<int>(a.n[0]);
+  const int64_t K = a.n[1], ldx = a.n[2];
+  const Segments<T> st(a);
+  const int64_t cols = SILU ? a.n[7] : st.total;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int fi = lane & 15, fg = lane >> 4;
+  const int kp = w % KS;
+  const int64_t tile = blockIdx.x * int64_t(TPB) + w / KS;
+  const bool tile_ok = tile * 16 < cols;
+  const int64_t n0 = tile_ok ? tile * 16 : 0;  // out-of-range tiles compute tile 0 and store nothing
+
+  // this lane's B rows (column n0 + fi) and its A row (input row fi)
+  int seg = 0;
+  int64_t idx = n0 + fi;
+  const uint4* wrow[NB];
+  if (SILU) {
+    wrow[0] = reinterpret_cast<const uint4*>(st.w[0] + idx * K);
+    wrow[1] = reinterpret_cast<const uint4*>(st.w[1] + idx * K);
+  } else {
+    seg = st.seg_of(n0);  // segments are multiples of 16 columns
+    idx = n0 - st.start(seg) + fi;
+    wrow[0] = reinterpret_cast<const uint4*>(st.weight(seg) + idx * K);
+  }
+  const int xr = fi < M ? fi : M - 1;
+  const uint4* xrow = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[0]) + xr * ldx);
+  const bool xlive = fi < M;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  const int64_t kv = K / 8;                 // 16-byte vectors per row
+  const int64_t steps = K / 32 / KS;        // k-steps of this wave
+  const int64_t v0 = kp * steps * 4;        // first vector of this wave's k range
+  const int64_t vend = v0 + steps * 4;
+  uint4 xa[2][kChunk], wb[2][NB][kChunk];
+  auto issue = [&](int buf, int64_t c) {
+#pragma unroll
+    for (int s = 0; s < kChunk; ++s) {
+      const int64_t v = v0 + (c + s) * 4 + fg;  // vector index: 32 columns per step, 8 per lane group
+      const int64_t vc = v < vend ? v : vend - 4 + fg;
+      xa[buf][s] = xrow[vc];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) wb[buf][b][s] = load_w<true>(wrow[b] + vc);
+    }
+  };
+  mf4v acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = mf4v{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf, int64_t c) {
+#pragma unroll
+    for (int s = 0; s < kChunk; ++s) {
+      const bool live = c + s < steps;
+      const uint4 xv = (live && xlive) ? xa[buf][s] : zero;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[b] = F::step(xv, live ? wb[buf][b][s] : zero, acc[b]);
+    }
+  };
+  (void)kv;
+  issue(0, 0);
+  for (int64_t c = 0; c < steps; c += 2 * kChunk) {
+    issue(1, c + kChunk);
+    compute(0, c);
+    if (c + kChunk >= steps) break;
+    issue(0, c + 2 * kChunk);
+    compute(1, c + kChunk);
+  }
+
+  // add the KS partial tiles of one column tile
+  if (KS > 1) {
+    const int t = w / KS;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (kp != 0) red[b][w][lane] = acc[b];
+    }
+    __syncthreads();
+    if (kp == 0) {
+#pragma unroll
+      for (int q = 1; q < KS; ++q)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] += red[b][t * KS + q][lane];
+    }
+  }
+  if (kp != 0 || !tile_ok) return;
+
+  // lane (fi, fg) holds D[4 fg + r][fi]: input row 4 fg + r, column n0 + fi
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * fg + r;
+    if (m >= M) break;
+    if (SILU) {
+      const float g = E::round(acc[0][r]);
+      const float u = E::round(acc[1][r]);
+      const float denom = E::round(E::round(expf(-g)) + 1.f);
+      st.out[0][m * st.ostride[0] + idx] = E::from_f(E::round(E::round(g / denom) * u));
+    } else {
+      float y = E::round(acc[0][r]);
+      const T* res = st.residual(seg);
+      if (res) y = E::round(E::to_f(res[m * st.res_stride(seg) + idx]) + y);
+      st.output(seg)[m * st.out_stride(seg) + idx] = E::from_f(y);
+    }
+  }
+}
+
+template <typename T, int KS>
+const void* pick_mfma_ks(bool silu) {
+  return silu ? reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, true>)
+              : reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, false>);
+}
+
+template <typename T>
+const void* pick_mfma(int ks, bool silu) {
+  switch (ks) {
+    case 1: return pick_mfma_ks<T, 1>(silu);
+    case 2: return pick_mfma_ks<T, 2>(silu);
+    default: return pick_mfma_ks<T, 4>(silu);
+  }
+}
+
 const char* plan_gemv(KArgs& a, Launch& l) {
   const int64_t M = a.n[0], K = a.n[1];
   const int dt = static_cast<int>(a.n[3]);
@@ -999,6 +1151,27 @@ const char* plan_gemv(KArgs& a, Launch& l) {
     }
     l.grid = dim3(static_cast<unsigned>(blocks));
     l.block = dim3(static_cast<unsigned>(64 * waves));
+    l.shmem = 0;
+    return nullptr;
+  }
+  // 2..16 rows of a 16-bit type without the prologue: the MFMA kernel.
+  // Every segment must be a whole number of 16-column tiles.
+  static const int mfma_knob = env_int("CHOMIK_HIP_GEMV_MFMA", 1);
+  bool tiles16 = true;
+  for (int s = 0; s < segs; ++s) tiles16 = tiles16 && a.n[7 + s] % 16 == 0;
+  if (mfma_knob && M >= 2 && M <= 16 && !pro && (dt == F16 || dt == BF16) && K % 32 == 0 && tiles16 &&
+      a.n[2] % 8 == 0 && aligned) {
+    const int64_t cols = silu ? a.n[7] : rows;
+    const int64_t tiles = cols / 16;
+    int ks = 1;  // split K over a block's waves until there are 256 blocks
+    while (ks < 4 && (tiles * ks + 3) / 4 < 256 && K / 32 / (ks * 2) >= 1) ks *= 2;
+    if (K % (32 * ks)) ks = 1;
+    const int64_t tpb = 4 / ks;
+    const int64_t blocks = (tiles + tpb - 1) / tpb;
+    if (blocks > 2147483647) return "gemv: too many rows";
+    l.func = dt == F16 ? pick_mfma<__half>(ks, silu) : pick_mfma<bf16_t>(ks, silu);
+    l.grid = dim3(static_cast<unsigned>(blocks));
+    l.block = dim3(256);
     l.shmem = 0;
     return nullptr;
   }

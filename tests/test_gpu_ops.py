@@ -127,7 +127,7 @@ def test_structural_program_cache_and_leaf_aliasing(hip):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, BFLOAT16])
-@pytest.mark.parametrize("rows", [1, 3, 8])
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
 def test_gemv_linear_variants(hip, dtype, rows):
     announce(f"gemv {np.dtype(dtype)} rows={rows}")
     rng = np.random.default_rng(rows)

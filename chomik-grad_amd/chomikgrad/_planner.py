@@ -26,6 +26,7 @@ Stages
 
 from __future__ import annotations
 
+import math
 import os
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Set, Tuple
@@ -59,8 +60,17 @@ GEMV_STAGE_BYTES = 48 * 1024
 GEMV_SPLIT = int(os.environ.get("CHOMIK_HIP_GEMV_SPLIT", "0"))
 # Decode attention: cache rows per workgroup = (32 for 2-byte, 16 for 4-byte
 # dtypes) x passes; 0 picks the passes from the shape, 1/2/4 forces them.
+# Decode attention: 0 chooses; 1, 2 or 4 force the chunk kernel with that
+# many passes per workgroup; -1 forces the streaming kernel.
 DECODE_ATTN_PASSES = int(os.environ.get("CHOMIK_HIP_ATTN_PASSES", "0"))
 DECODE_ATTN_MAX_CHUNKS = 64
+# The streaming kernel takes over when the chunk kernel would need more than
+# this many workgroups (several latency-bound rounds); it launches about
+# DECODE_ATTN_STREAM_WGS workgroups with DECODE_ATTN_STREAM_UNROLL passes
+# per tile (2 or 4; 2 measured faster at batch 8 over 4096 cached rows).
+DECODE_ATTN_STREAM_ABOVE = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_ABOVE", "768"))
+DECODE_ATTN_STREAM_WGS = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_WGS", "768"))
+DECODE_ATTN_STREAM_UNROLL = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_UNROLL", "2"))
 SDPA_MAX_KEYS = 32768
 ARENA_ALIGN = 256
 SUPPORTED_TAGS = frozenset({"rms_norm", "rope", "sdpa", "softmax"})
@@ -994,12 +1004,13 @@ def decode_attention_rows(itemsize: int) -> int:
 
 
 def decode_attention_passes(B: int, KV: int, C: int, itemsize: int) -> int:
-    """Passes (rows per workgroup / rows per pass) for the split-context
-    decode attention: the most rows per workgroup that still leaves >= 1024
-    workgroups, else one pass (short caches: as many workgroups as rows
-    allow, so the per-workgroup latency chain stays short)."""
+    """Passes (rows per workgroup / rows per pass) for the chunk kernel of
+    the split-context decode attention: the most rows per workgroup that
+    still leaves >= 1024 workgroups, else one pass (short caches: as many
+    workgroups as rows allow, so the per-workgroup latency chain stays
+    short)."""
     rows = decode_attention_rows(itemsize)
-    if DECODE_ATTN_PASSES:
+    if DECODE_ATTN_PASSES > 0:
         chosen = DECODE_ATTN_PASSES
     else:
         chosen = 1
@@ -1011,6 +1022,29 @@ def decode_attention_passes(B: int, KV: int, C: int, itemsize: int) -> int:
     while chosen < 4 and -(-C // (rows * chosen)) > DECODE_ATTN_MAX_CHUNKS:
         chosen *= 2
     return chosen
+
+
+def decode_attention_plan(B: int, KV: int, C: int, G: int, itemsize: int, divisor: float = 8.0) -> Dict[str, int]:
+    """Kernel choice for the fused decode attention: ``passes`` > 0 is the
+    chunk kernel (``chunks`` workgroups per KV head); ``passes`` 0 is the
+    streaming kernel, whose ``chunks`` workgroups per KV head each stream
+    ``rows`` cache rows in tiles of ``unroll`` passes."""
+    rpp = decode_attention_rows(itemsize)
+    stream = DECODE_ATTN_PASSES == -1
+    if DECODE_ATTN_PASSES == 0:
+        biggest = -(-C // (rpp * 4))
+        stream = B * KV * biggest > DECODE_ATTN_STREAM_ABOVE or biggest > DECODE_ATTN_MAX_CHUNKS
+    # the streaming kernel multiplies by the reciprocal of the score divisor,
+    # exact only for a power of two (the usual sqrt(64) = 8)
+    stream = stream and divisor > 0 and math.frexp(divisor)[0] == 0.5
+    if not stream:
+        passes = decode_attention_passes(B, KV, C, itemsize)
+        return {"passes": passes, "chunks": -(-C // (rpp * passes)), "rows": 0, "unroll": 0}
+    target = max(1, min(DECODE_ATTN_MAX_CHUNKS, -(-DECODE_ATTN_STREAM_WGS // (B * KV))))
+    rows = -(-C // target)
+    rows = -(-rows // rpp) * rpp
+    unroll = DECODE_ATTN_STREAM_UNROLL
+    return {"passes": 0, "chunks": -(-C // rows), "rows": rows, "unroll": unroll}
 
 
 def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitter") -> List[Step]:
@@ -1063,8 +1097,8 @@ def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitte
             continue
         if tickets is None or tickets.size < B * KV:
             tickets = emitter.zeros(4 * max(B * KV, 64), "tickets")
-        passes = decode_attention_passes(B, KV, C, q.itemsize)
-        chunks = -(-C // (decode_attention_rows(q.itemsize) * passes))
+        plan = decode_attention_plan(B, KV, C, H // KV, q.itemsize, float(step.attrs["divisor"]))
+        chunks = plan["chunks"]
         if chunks > DECODE_ATTN_MAX_CHUNKS:
             continue
         floats = B * H * chunks * 66 if chunks > 1 else 1
@@ -1075,7 +1109,8 @@ def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitte
                       partials[floats]],
                      [step.outs[0], wk.outs[0], wv.outs[0]],
                      {"in_place": wk.attrs["in_place"], "table_length": rq.attrs["table_length"],
-                      "mode": rq.attrs["mode"], "divisor": step.attrs["divisor"], "passes": passes})
+                      "mode": rq.attrs["mode"], "divisor": step.attrs["divisor"], "passes": plan["passes"],
+                      "stream_rows": plan["rows"], "unroll": plan["unroll"]})
         steps[index] = fused
         removed.update({id(rq), id(rk), id(wk), id(wv)})
     return [s for s in steps if id(s) not in removed]
@@ -1244,8 +1279,10 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         x, w = step.ins
         out = step.outs[0]
         rows = _prod(x.shape[:-1])
+        aligned = all(_ptr(pv)[1] % 16 == 0 for pv in (x, w, out))
         return kind, [_ptr(x), _ptr(w), _ptr(out)], [
-            rows, x.shape[-1], x.row_stride(), dtype_code(x.dtype), dtype_code(w.dtype)], [a["eps"]]
+            rows, x.shape[-1], x.row_stride(), dtype_code(x.dtype), dtype_code(w.dtype),
+            1 if aligned else 0], [a["eps"]]
     if kind == K_ROPE:
         x, position, table = step.ins
         out = step.outs[0]
@@ -1298,7 +1335,7 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
                 v.strides[0], v.strides[1], v.strides[3],
                 a["mode"], a["table_length"]] + list(cache_k.strides)
         ints += [ws[0], ws[2], ms[0], ms[1], ms[3], dtype_code(mask.dtype), dtype_code(w.dtype),
-                 1 if a["in_place"] else 0, a["passes"]]
+                 1 if a["in_place"] else 0, a["passes"], a["stream_rows"], a["unroll"]]
         ptrs = [_ptr(pv) for pv in (q, k, v, position, table, cache_k, cache_v, w, mask, out, out_k, out_v,
                                     tickets, partials)]
         return kind, ptrs, ints, [a["divisor"]]

@@ -54,12 +54,12 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t bits) {
   return __uint_as_float(static_cast<uint32_t>(bits) << 16);
 }
 
-// float32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+// float32 -> bfloat16 bits, round to nearest even, NaN -> quiet NaN with the
+// upper payload bits kept ((u >> 16) | 0x40).  gfx950's v_cvt_pk_bf16_f32
+// gives exactly these bits for every 32-bit input (checked exhaustively on
+// an MI355X), in one instruction and without a branch.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float value) {
-  uint32_t u = __float_as_uint(value);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(value));
 }
 
 __device__ __forceinline__ float round_f16(float v) { return __half2float(__float2half(v)); }

@@ -31,7 +31,9 @@
 #include "chip.h"
 #include "chomik_hip.h"
 
+#include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 namespace chip {
 namespace {
@@ -96,6 +98,94 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Called by every workgroup of (sequence b, KV head g) after it stored its
+// partials (P V sums, maximum and exp-sum per query head of the group): the
+// last of the NS workgroups to arrive -- a self-resetting atomic ticket, no
+// spinning -- merges the NS splits and writes the G output rows.
+template <typename T, int G>
+__device__ __forceinline__ void combine_chunks(const KArgs& a, int64_t b, int64_t g, int64_t NS) {
+  using E = Elem<T>;
+  constexpr int QT = (G * kHead + kThreads - 1) / kThreads;  // output values per thread
+  __shared__ float fac[G][kMaxChunks];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t B = a.n[0], H = a.n[1], KV = a.n[2];
+  float* partials = static_cast<float*>(a.p[13]);
+  const int64_t total = B * H * NS;
+  T* out = static_cast<T*>(a.p[9]);
+
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();                // ... and every other thread's
+  if (tid == 0) {
+    int* tickets = static_cast<int*>(a.p[12]);
+    const int ticket = __hip_atomic_fetch_add(&tickets[b * KV + g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = ticket == static_cast<int>(NS) - 1;
+    if (last)  // reset for the next launch
+      __hip_atomic_store(&tickets[b * KV + g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  // Every partial load is issued before the first use (one round trip) and
+  // without branches (chunk indices clamped; the extra terms get factor 0):
+  // first the chunk maxima and exp-sums (one wave per head, one lane per
+  // chunk), then this thread's P V sums.
+  constexpr int HW = (G + kThreads / 64 - 1) / (kThreads / 64);  // heads per wave
+  const int64_t head0 = (b * H + g * G) * NS;
+  const int nlast = static_cast<int>(NS) - 1;
+  const int kc = lane < nlast ? lane : nlast;
+  float mk_[HW], lk_[HW];
+#pragma unroll
+  for (int x = 0; x < HW; ++x) {
+    const int h = wave + (kThreads / 64) * x;
+    const int64_t at = head0 + (h < G ? h : 0) * NS + kc;
+    mk_[x] = load_agent(partials + total * kHead + at);
+    lk_[x] = load_agent(partials + total * (kHead + 1) + at);
+  }
+  float ov[QT][kMaxChunks];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;
+    const int h = (i / kHead) < G ? i / kHead : 0;
+    const float* Op = partials + (head0 + h * NS) * kHead + lane;
+#pragma unroll
+    for (int k0 = 0; k0 < kMaxChunks; k0 += 8) {
+      if (k0 >= NS) break;  // uniform: only the blocks of 8 chunks that exist
+#pragma unroll
+      for (int k = k0; k < k0 + 8; ++k) ov[t][k] = load_agent(Op + (k < nlast ? k : nlast) * kHead);
+    }
+  }
+  // per head: m = max over chunks; weights exp(M_k - m) / sum_k L_k exp(M_k - m)
+#pragma unroll
+  for (int x = 0; x < HW; ++x) {
+    const int h = wave + (kThreads / 64) * x;
+    if (h >= G) break;
+    const float mk = lane < NS ? mk_[x] : -INFINITY;
+    float m = mk;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = nan_max(m, __shfl_xor(m, o, 64));
+    const float f = lane < NS ? __expf(mk - m) : 0.f;
+    float l = lane < NS ? lk_[x] * f : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    fac[h][lane] = f / l;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;
+    if (i >= G * kHead) continue;
+    const float* F = fac[i / kHead];
+    float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k0 = 0; k0 < kMaxChunks; k0 += 8) {
+      if (k0 >= NS) break;
+#pragma unroll
+      for (int k = k0; k < k0 + 8; ++k) o4[k & 3] = fmaf(ov[t][k], F[k], o4[k & 3]);
+    }
+    out[(b * H + g * G + i / kHead) * kHead + lane] = E::from_f((o4[0] + o4[1]) + (o4[2] + o4[3]));
+  }
+}
+
 // p[0] q, p[1] k, p[2] v (linear outputs, strided views), p[3] positions
 // (int32), p[4] RoPE table (len, 64), p[5] K cache in, p[6] V cache in,
 // p[7] write mask, p[8] attention mask (or null), p[9] out (B, H, 1, 64),
@@ -124,8 +214,6 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
   __shared__ float vsh[R][kHead];
   __shared__ float red[kThreads / 64][G], red2[kThreads / 64][G];
   __shared__ float mh[G], lh[G];
-  __shared__ float fac[G][kMaxChunks];
-  __shared__ int last;
 
   const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
   const int64_t NS = (C + R - 1) / R;
@@ -363,78 +451,394 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
     reinterpret_cast<uint4*>(Vo + dst)[part] = vvec;
   }
   if (NS == 1) return;
+  combine_chunks<T, G>(a, b, g, NS);
+}
 
-  // -- the last workgroup of (b, g) to finish combines the chunks.
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();                // ... and every other thread's
-  if (tid == 0) {
-    int* tickets = static_cast<int*>(a.p[12]);
-    const int ticket = __hip_atomic_fetch_add(&tickets[b * KV + g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = ticket == static_cast<int>(NS) - 1;
-    if (last)  // reset for the next launch
-      __hip_atomic_store(&tickets[b * KV + g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// ------------------------------------------------------------ long caches
+// q . k over one 16-byte row slice with q kept packed in the cache dtype:
+// v_dot2 for 16-bit types (products of half-precision values are exact in
+// float32, accumulated in float32), fmaf for float32.
+template <typename T> struct RowDot;
+typedef _Float16 dh2 __attribute__((ext_vector_type(2)));
+typedef __bf16 db2 __attribute__((ext_vector_type(2)));
+template <> struct RowDot<__half> {
+  __device__ static __forceinline__ float dot(const uint4& k, const uint4& q) {
+    float acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(dh2, k.x), __builtin_bit_cast(dh2, q.x), 0.f, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(dh2, k.y), __builtin_bit_cast(dh2, q.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(dh2, k.z), __builtin_bit_cast(dh2, q.z), acc, false);
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(dh2, k.w), __builtin_bit_cast(dh2, q.w), acc, false);
   }
-  __syncthreads();
-  if (!last) return;
-  // Every partial load is issued before the first use (one round trip) and
-  // without branches (chunk indices clamped; the extra terms get factor 0):
-  // first the chunk maxima and exp-sums (one wave per head, one lane per
-  // chunk), then this thread's P V sums.
-  constexpr int HW = (G + kThreads / 64 - 1) / (kThreads / 64);  // heads per wave
-  const int64_t head0 = (b * H + g * G) * NS;
-  const int nlast = static_cast<int>(NS) - 1;
-  const int kc = lane < nlast ? lane : nlast;
-  float mk_[HW], lk_[HW];
+};
+template <> struct RowDot<bf16_t> {
+  __device__ static __forceinline__ float dot(const uint4& k, const uint4& q) {
+    float acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(db2, k.x), __builtin_bit_cast(db2, q.x), 0.f, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(db2, k.y), __builtin_bit_cast(db2, q.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(db2, k.z), __builtin_bit_cast(db2, q.z), acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(db2, k.w), __builtin_bit_cast(db2, q.w), acc, false);
+  }
+};
+template <> struct RowDot<float> {
+  __device__ static __forceinline__ float dot(const uint4& k, const uint4& q) {
+    float acc = __uint_as_float(k.x) * __uint_as_float(q.x);
+    acc = fmaf(__uint_as_float(k.y), __uint_as_float(q.y), acc);
+    acc = fmaf(__uint_as_float(k.z), __uint_as_float(q.z), acc);
+    return fmaf(__uint_as_float(k.w), __uint_as_float(q.w), acc);
+  }
+};
+
+// Buffer resource over [base, base + bytes) addressed by 32-bit byte
+// offsets (gfx9-family descriptor); loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+template <typename T>
+__device__ __forceinline__ float buffer_scalar(__amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (sizeof(T) == 2)
+    return Elem<T>::to_f(__builtin_bit_cast(T, static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0))));
+  else
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ uint4 buffer_row(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// The chunk kernel gives every workgroup one chunk of at most 128 rows: for
+// short caches its one latency chain is the kernel's time, but a long cache
+// becomes thousands of workgroups that run in several latency-bound rounds.
+// Here a workgroup owns a range of L rows (n[29], a multiple of the rows per
+// pass; NS = ceil(C / L) ranges per (sequence, KV head)) and streams it in
+// tiles of U passes.  K and V are staggered so that one register set of each
+// suffices: the next tile's K rows (with its write-mask and mask values) are
+// loaded as soon as the current tile is scored, and its V rows as soon as the
+// current tile is accumulated, so each load has the other half's work to
+// arrive.  Loads are buffer loads at loop-invariant 32-bit offsets plus the
+// tile's offset; rows past the cache read 0, and the prefetch after the last
+// tile uses an out-of-range offset (zeros, no memory traffic), so the loop
+// has no peeled tail.  Each row group (the LPR lanes
+// sharing a row) keeps an online softmax per query head -- running maximum
+// and exp-sum, rescaled once per tile -- and its lanes' slices of P V in
+// registers, so V is never staged in LDS.  A tile without blended rows (the
+// common case in place: only the new token's row has w != 0) takes a path
+// without the blend and the cache stores, chosen once per wave.  At the end
+// the row groups of a wave merge by shuffles and the waves through LDS; the
+// workgroup writes the chunk kernel's partials (or the output, when one
+// range covers the cache) and the same combine follows.  Scores, blended
+// rows and cache writes keep the chunk kernel's rounding; the score divisor
+// must be a power of two (sqrt(64) = 8), whose reciprocal multiplies exactly.
+template <typename T, int G, int U>
+__global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
+  using E = Elem<T>;
+  constexpr int S = static_cast<int>(sizeof(T));
+  constexpr int V = 16 / S;                  // elements per vector
+  constexpr int LPR = kHead / V;             // lanes per row
+  constexpr int RPP = kThreads / LPR;        // row groups = rows per pass
+  constexpr int GPW = 64 / LPR;              // row groups per wave
+  constexpr int TR = RPP * U;                // rows per tile
+  constexpr int NW = kThreads / 64;
+  constexpr int QT = (G * kHead + kThreads - 1) / kThreads;
+
+  __shared__ float qs[G][kHead];
+  __shared__ float ks[kHead], vs[kHead];
+  __shared__ float wmax[NW][G], wsum[NW][G];
+  __shared__ float wacc[NW][G][kHead];
+
+  const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
+  const int64_t L = a.n[29];
+  const int64_t NS = (C + L - 1) / L;
+  const int64_t split = blockIdx.x % NS, bg = blockIdx.x / NS;
+  const int64_t b = bg / KV, g = bg % KV;
+  const int dt = E::code;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int part = lane % LPR;
+  const int rgi = wave * GPW + lane / LPR;  // this lane's row group
+  const int64_t c0 = split * L;
+  const int64_t c1 = c0 + L < C ? c0 + L : C;
+  const int64_t ntiles = (c1 - c0 + TR - 1) / TR;
+  const int64_t cb = b * a.n[16] + g * a.n[17];
+  const int64_t wb = b * a.n[20], wc = a.n[21];
+  const bool masked = a.p[8] != nullptr;
+  const bool in_place = a.n[27] != 0;
+  const int head = scatter_head<G, LPR>(part);
+  const T* Wm = static_cast<const T*>(a.p[7]);
+  // Without a mask the mask loads read the write mask (always bound) and
+  // are replaced by 0: no branch around a load.  Resource bases are uniform
+  // (this sequence and KV head); the lane's query head is an offset.
+  const T* Am = masked ? static_cast<const T*>(a.p[8]) + b * a.n[22] + g * G * a.n[23] : Wm + wb;
+  const int64_t mh = masked ? a.n[23] : 0, mc = masked ? a.n[24] : wc;
+  const auto krs = buffer_over(static_cast<const T*>(a.p[5]) + cb, C * kHead * S);
+  const auto vrs = buffer_over(static_cast<const T*>(a.p[6]) + cb, C * kHead * S);
+  const auto wrs = buffer_over(Wm + wb, ((C - 1) * wc + 1) * S);
+  const auto mrs = buffer_over(Am, ((G - 1) * mh + (C - 1) * mc + 1) * S);
+  int koff[U], woff[U], moff[U];  // byte offsets of this lane's rows within a tile
 #pragma unroll
-  for (int x = 0; x < HW; ++x) {
-    const int h = wave + (kThreads / 64) * x;
-    const int64_t at = head0 + (h < G ? h : 0) * NS + kc;
-    mk_[x] = load_agent(partials + total * kHead + at);
-    lk_[x] = load_agent(partials + total * (kHead + 1) + at);
+  for (int u = 0; u < U; ++u) {
+    const int r = u * RPP + rgi;
+    koff[u] = (r * kHead + part * V) * S;
+    woff[u] = static_cast<int>(r * wc * S);
+    moff[u] = static_cast<int>((head * mh + r * mc) * S);
   }
-  float ov[QT][kMaxChunks];
+
+  uint4 kbuf[U], vbuf[U];
+  float wbuf[U], mbuf[U];
+  // Tile t's loads; past the last tile every offset is out of range, so
+  // the loads return 0 without touching memory.
+  constexpr int kPast = 0x7fff0000;
+  auto issue_k = [&](int64_t t) {
+    const int64_t r0 = c0 + t * TR;
+    const bool in = t < ntiles;
+    const int tk = in ? static_cast<int>(r0 * kHead * S) : kPast, tw = in ? static_cast<int>(r0 * wc * S) : kPast,
+              tm = in ? static_cast<int>(r0 * mc * S) : kPast;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      kbuf[u] = buffer_row(krs, koff[u] + tk);
+      wbuf[u] = buffer_scalar<T>(wrs, woff[u] + tw);
+      const float mv = buffer_scalar<T>(mrs, moff[u] + tm);
+      mbuf[u] = masked ? mv : 0.f;
+    }
+  };
+  auto issue_v = [&](int64_t t) {
+    const int tk = t < ntiles ? static_cast<int>((c0 + t * TR) * kHead * S) : kPast;
+#pragma unroll
+    for (int u = 0; u < U; ++u) vbuf[u] = buffer_row(vrs, koff[u] + tk);
+  };
+  issue_k(0);
+  issue_v(0);
+
+  // -- RoPE of q and k (the position load, then the table).
+  const int32_t* positions = static_cast<const int32_t*>(a.p[3]);
+  int64_t pos = a.n[14] == 2 ? positions[b] : positions[0];
+  float xq[QT];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int i = tid + kThreads * t;
-    const int h = (i / kHead) < G ? i / kHead : 0;
-    const float* Op = partials + (head0 + h * NS) * kHead + lane;
+    xq[t] = i < G * kHead ? load_f(a.p[0], b * a.n[5] + (g * G + i / kHead) * a.n[6] + lane * a.n[7], dt) : 0.f;
+  }
+  float xk = 0.f, xv = 0.f;
+  if (tid < kHead) {
+    xk = load_f(a.p[1], b * a.n[8] + g * a.n[9] + tid * a.n[10], dt);
+    xv = load_f(a.p[2], b * a.n[11] + g * a.n[12] + tid * a.n[13], dt);
+  }
+  if (!(pos >= 0 && pos < a.n[15])) {
+    if (tid == 0) raise_error(a, ERR_POSITION);
+    pos = 0;
+  }
+  {
+    const int i = lane & 31;
+    const float c = load_f(a.p[4], pos * kHead + i, dt);
+    const float sn = load_f(a.p[4], pos * kHead + 32 + i, dt);
+    auto rope = [&](float x) {
+      const float p = __shfl_xor(x, 32, 64);
+      return E::round(lane < 32 ? __fadd_rn(__fmul_rn(x, c), __fmul_rn(p, -sn))
+                                : __fadd_rn(__fmul_rn(p, sn), __fmul_rn(x, c)));
+    };
 #pragma unroll
-    for (int k0 = 0; k0 < kMaxChunks; k0 += 8) {
-      if (k0 >= NS) break;  // uniform: only the blocks of 8 chunks that exist
-#pragma unroll
-      for (int k = k0; k < k0 + 8; ++k) ov[t][k] = load_agent(Op + (k < nlast ? k : nlast) * kHead);
+    for (int t = 0; t < QT; ++t) {
+      const int i2 = tid + kThreads * t;
+      const float r = rope(xq[t]);
+      if (i2 < G * kHead) qs[i2 / kHead][lane] = r;
+    }
+    const float rk = rope(xk);
+    if (tid < kHead) {
+      ks[tid] = rk;
+      vs[tid] = xv;
     }
   }
-  // per head: m = max over chunks; weights exp(M_k - m) / sum_k L_k exp(M_k - m)
+  __syncthreads();
+  uint4 qp[G];  // this lane's slice of every head's q, packed in T (exact: q is rounded to T)
 #pragma unroll
-  for (int x = 0; x < HW; ++x) {
-    const int h = wave + (kThreads / 64) * x;
-    if (h >= G) break;
-    const float mk = lane < NS ? mk_[x] : -INFINITY;
-    float m = mk;
+  for (int h = 0; h < G; ++h) qp[h] = pack<T>(&qs[h][part * V]);
+  const float rdiv = 1.f / E::round(a.f[0]);  // exact: the divisor is a power of two
+
+  float m[G], l[G], acc[G][V];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = nan_max(m, __shfl_xor(m, o, 64));
-    const float f = lane < NS ? __expf(mk - m) : 0.f;
-    float l = lane < NS ? lk_[x] * f : 0.f;
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-    fac[h][lane] = f / l;
+    for (int e = 0; e < V; ++e) acc[h][e] = 0.f;
+  }
+  // the new token's k' and v slices of this lane, packed in T (exact)
+  const uint4 knew = pack<T>(&ks[part * V]), vnew = pack<T>(&vs[part * V]);
+  // Blend of a cache row with the new row.  The fresh values pass through an
+  // empty asm first, so nothing derived from them is hoisted out of the rare
+  // slow path into registers held across the whole loop.
+  auto blend = [&](uint4& row, float w, uint4 fresh) {
+    asm volatile("" : "+v"(fresh.x), "+v"(fresh.y), "+v"(fresh.z), "+v"(fresh.w));
+    float x[V], f[V];
+    unpack<T>(row, x);
+    unpack<T>(fresh, f);
+    const float keep = E::round(1.f - w);
+#pragma unroll
+    for (int e = 0; e < V; ++e) x[e] = E::round(E::round(x[e] * keep) + E::round(f[e] * w));
+    row = pack<T>(x);
+  };
+  T* Ko = static_cast<T*>(a.p[10]);
+  T* Vo = static_cast<T*>(a.p[11]);
+  // the cache row of row j: in place, or the new buffer's contiguous layout
+  auto dst_row = [&](int64_t j) { return in_place ? cb + j * kHead : ((b * KV + g) * C + j) * kHead; };
+
+  float s[U][G], wt[U];
+  // Slow path of a tile (chosen once per wave): the rows with w != 0 are
+  // blended in their register buffers and written to the cache (every row
+  // is written when the cache goes to a new buffer); the shared scoring and
+  // accumulation below then see the blended rows.
+  auto prep_k = [&](int64_t t) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      const float w = wbuf[u];
+      if (w != 0.f) blend(kbuf[u], w, knew);
+      if (j < c1 && (!in_place || w != 0.f)) reinterpret_cast<uint4*>(Ko + dst_row(j))[part] = kbuf[u];
+    }
+  };
+  auto prep_v = [&](int64_t t) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      const float w = wt[u];
+      if (w != 0.f) blend(vbuf[u], w, vnew);
+      if (j < c1 && (!in_place || w != 0.f)) reinterpret_cast<uint4*>(Vo + dst_row(j))[part] = vbuf[u];
+    }
+  };
+  // Scores of the tile's U rows for all G heads (the reduce-scatter leaves
+  // each lane one head's dot product; the row group then shares them) and
+  // one rescale of the running state.
+  auto score = [&](int64_t t) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      wt[u] = wbuf[u];
+      float d[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) d[h] = RowDot<T>::dot(kbuf[u], qp[h]);
+      float sc = E::round(E::round(reduce_scatter<G, LPR>(d, part)) * rdiv);
+      sc = E::round(sc + mbuf[u]);
+      sc = j < c1 ? sc : -INFINITY;
+#pragma unroll
+      for (int h = 0; h < G; ++h) s[u][h] = G == 1 ? sc : __shfl(sc, (lane & ~(LPR - 1)) + h * (LPR / G), 64);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mt = m[h];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mt = nan_max(mt, s[u][h]);
+      const float f = mt == m[h] ? 1.f : __expf(m[h] - mt);
+      m[h] = mt;
+      l[h] *= f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[h][e] *= f;
+    }
+  };
+  // exp-sums and P V of the tile's rows.
+  auto accumulate = [&](int64_t t) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      float vf[V];
+      unpack<T>(j < c1 ? vbuf[u] : make_uint4(0, 0, 0, 0), vf);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float p = s[u][h] == -INFINITY ? 0.f : __expf(s[u][h] - m[h]);
+        l[h] += p;
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
+      }
+    }
+  };
+  // blended rows or a copied cache make the tile slow, for the whole wave
+  auto slow_tile = [&]() {
+    bool any = !in_place;
+#pragma unroll
+    for (int u = 0; u < U; ++u) any = any || wbuf[u] != 0.f;
+    return __any(any) != 0;
+  };
+
+  for (int64_t t = 0; t < ntiles; ++t) {
+    const bool slow = slow_tile();
+    if (slow) prep_k(t);
+    score(t);
+    issue_k(t + 1);
+    if (slow) prep_v(t);
+    accumulate(t);
+    issue_v(t + 1);
+  }
+
+  // -- merge the row groups of each wave (shuffles), then the waves (LDS).
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float M = m[h];
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1) M = nan_max(M, __shfl_xor(M, o, 64));
+    const float f = M == m[h] ? 1.f : __expf(m[h] - M);
+    float ls = l[h] * f;
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1) ls += __shfl_xor(ls, o, 64);
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      float x = acc[h][e] * f;
+#pragma unroll
+      for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
+      acc[h][e] = x;
+    }
+    if (lane < LPR) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) wacc[wave][h][part * V + e] = acc[h][e];
+      if (part == 0) {
+        wmax[wave][h] = M;
+        wsum[wave][h] = ls;
+      }
+    }
   }
   __syncthreads();
+
+  float* partials = static_cast<float*>(a.p[13]);
+  const int64_t total = B * H * NS;
+  T* out = static_cast<T*>(a.p[9]);
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int i = tid + kThreads * t;
     if (i >= G * kHead) continue;
-    const float* F = fac[i / kHead];
-    float o4[4] = {0.f, 0.f, 0.f, 0.f};
+    const int h = i / kHead;
+    float M = wmax[0][h];
 #pragma unroll
-    for (int k0 = 0; k0 < kMaxChunks; k0 += 8) {
-      if (k0 >= NS) break;
+    for (int w = 1; w < NW; ++w) M = nan_max(M, wmax[w][h]);
+    float o = 0.f, ls = 0.f;
 #pragma unroll
-      for (int k = k0; k < k0 + 8; ++k) o4[k & 3] = fmaf(ov[t][k], F[k], o4[k & 3]);
+    for (int w = 0; w < NW; ++w) {
+      const float f = wmax[w][h] == M ? 1.f : __expf(wmax[w][h] - M);
+      o = fmaf(wacc[w][h][lane], f, o);
+      ls = fmaf(wsum[w][h], f, ls);
     }
-    out[(b * H + g * G + i / kHead) * kHead + lane] = E::from_f((o4[0] + o4[1]) + (o4[2] + o4[3]));
+    if (NS == 1) {
+      out[(b * H + g * G + h) * kHead + lane] = E::from_f(o / ls);
+    } else {
+      const int64_t row = (b * H + g * G + h) * NS + split;
+      store_agent(partials + row * kHead + lane, o);
+      if (lane == 0) {
+        store_agent(partials + total * kHead + row, M);
+        store_agent(partials + total * (kHead + 1) + row, ls);
+      }
+    }
   }
+  if (NS == 1) return;
+  combine_chunks<T, G>(a, b, g, NS);
+}
+
+template <typename T, int G>
+const void* pick_stream(int u) {
+  return u == 2 ? reinterpret_cast<const void*>(&k_decode_attn_stream<T, G, 2>)
+                : reinterpret_cast<const void*>(&k_decode_attn_stream<T, G, 4>);
+}
+
+template <typename T>
+const void* pick_stream_g(int64_t G, int u) {
+  switch (G) {
+    case 1: return pick_stream<T, 1>(u);
+    case 2: return pick_stream<T, 2>(u);
+    case 4: return pick_stream<T, 4>(u);
+    case 8: return pick_stream<T, 8>(u);
+  }
+  return nullptr;
 }
 
 template <typename T, int G>
@@ -465,7 +869,37 @@ const char* plan_decode_attn(KArgs& a, Launch& l) {
   if (a.n[14] != 1 && a.n[14] != 2) return "decode_attn: position input required";
   if (a.n[25] != a.n[4] || a.n[26] != a.n[4]) return "decode_attn: masks must have the model dtype";
   const int np = static_cast<int>(a.n[28]);
-  if (np != 1 && np != 2 && np != 4) return "decode_attn: passes per workgroup must be 1, 2 or 4";
+  if (np == 0) {  // streaming kernel: n[29] rows per workgroup, n[30] passes per tile
+    const int64_t rpp = a.n[4] == F32 ? 16 : 32, L = a.n[29];
+    const int u = static_cast<int>(a.n[30]);
+    if (L <= 0 || L % rpp) return "decode_attn: rows per workgroup must be a positive multiple of the rows per pass";
+    if (u != 2 && u != 4) return "decode_attn: passes per tile must be 2 or 4";
+    if ((C + L - 1) / L > kMaxChunks) return "decode_attn: more than 64 cache ranges per KV head";
+    int e2 = 0;
+    if (!(a.f[0] > 0.f) || std::frexp(a.f[0], &e2) != 0.5f)
+      return "decode_attn: the streaming kernel needs a power-of-two score divisor";
+    // 32-bit buffer offsets, with room for the last tile's rows past the end
+    const int64_t esize = a.n[4] == F32 ? 4 : 2, span = C + 256;
+    if (a.n[21] < 0 || a.n[23] < 0 || a.n[24] < 0 ||
+        span * kHead * esize > 2147483647 || span * std::max<int64_t>(a.n[21], a.n[24]) * esize > 2147483647 ||
+        (H / KV) * a.n[23] * esize > 2147483647 - span * a.n[24] * esize)
+      return "decode_attn: cache, write mask and mask must span less than 2 GiB per (sequence, KV head)";
+    switch (a.n[4]) {
+      case F32: l.func = pick_stream_g<float>(H / KV, u); break;
+      case F16: l.func = pick_stream_g<__half>(H / KV, u); break;
+      case BF16: l.func = pick_stream_g<bf16_t>(H / KV, u); break;
+      default: return "decode_attn: float dtype required";
+    }
+    if (!l.func) return "decode_attn: query heads per KV head must be 1, 2, 4 or 8";
+    const int64_t blocks = B * KV * ((C + L - 1) / L);
+    if (blocks > 2147483647) return "decode_attn: too many workgroups";
+    l.grid = dim3(static_cast<unsigned>(blocks));
+    l.block = dim3(kThreads);
+    l.shmem = 0;
+    a.p[kErrPtr] = device_error_word();
+    return nullptr;
+  }
+  if (np != 1 && np != 2 && np != 4) return "decode_attn: passes per workgroup must be 0, 1, 2 or 4";
   if ((C + (a.n[4] == F32 ? 16 : 32) * np - 1) / ((a.n[4] == F32 ? 16 : 32) * np) > kMaxChunks)
     return "decode_attn: more than 64 cache chunks per KV head";
   switch (a.n[4]) {

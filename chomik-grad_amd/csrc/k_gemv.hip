@@ -962,12 +962,12 @@ template <> struct SkinnyMfma<bf16_t> {
 constexpr int kChunk = 4;  // k-steps of 32 per register buffer
 
 template <typename T, int KS, bool SILU>
-__global__ __launch_bounds__(256) void k_gemv_mfma(KArgs a) {
+__global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) {
   using E = Elem<T>;
   using F = SkinnyMfma<T>;
-  constexpr int TPB = 4 / KS;        // column tiles per block
-  constexpr int NB = SILU ? 2 : 1;   // B operands (gate, up)
-  __shared__ mf4v red[SILU ? 2 : 1][4][64];
+  constexpr int TPB = KS >= 4 ? 1 : 4 / KS;  // column tiles per block
+  constexpr int NB = SILU ? 2 : 1;           // B operands (gate, up)
+  __shared__ mf4v red[SILU ? 2 : 1][KS * TPB][64];
 
   const int M = static_cast<int>(a.n[0]);
   const int64_t K = a.n[1], ldx = a.n[2];
@@ -1081,7 +1081,9 @@ const void* pick_mfma(int ks, bool silu) {
   switch (ks) {
     case 1: return pick_mfma_ks<T, 1>(silu);
     case 2: return pick_mfma_ks<T, 2>(silu);
-    default: return pick_mfma_ks<T, 4>(silu);
+    case 4: return pick_mfma_ks<T, 4>(silu);
+    case 8: return pick_mfma_ks<T, 8>(silu);
+    default: return pick_mfma_ks<T, 16>(silu);
   }
 }
 
@@ -1163,15 +1165,19 @@ const char* plan_gemv(KArgs& a, Launch& l) {
       a.n[2] % 8 == 0 && aligned) {
     const int64_t cols = silu ? a.n[7] : rows;
     const int64_t tiles = cols / 16;
-    int ks = 1;  // split K over a block's waves until there are 256 blocks
-    while (ks < 4 && (tiles * ks + 3) / 4 < 256 && K / 32 / (ks * 2) >= 1) ks *= 2;
-    if (K % (32 * ks)) ks = 1;
-    const int64_t tpb = 4 / ks;
+    // Split K over up to 16 waves of a block while the launch has fewer
+    // than 2048 waves and each wave keeps at least one register chunk.
+    static const int max_ks = env_int("CHOMIK_HIP_GEMV_MFMA_SPLIT", 16);
+    const int64_t ksteps = K / 32;
+    int ks = 1;
+    while (ks < max_ks && ks < 16 && tiles * ks < 2048 && ksteps % (ks * 2) == 0 && ksteps / (ks * 2) >= kChunk)
+      ks *= 2;
+    const int64_t tpb = ks >= 4 ? 1 : 4 / ks;
     const int64_t blocks = (tiles + tpb - 1) / tpb;
     if (blocks > 2147483647) return "gemv: too many rows";
     l.func = dt == F16 ? pick_mfma<__half>(ks, silu) : pick_mfma<bf16_t>(ks, silu);
     l.grid = dim3(static_cast<unsigned>(blocks));
-    l.block = dim3(256);
+    l.block = dim3(static_cast<unsigned>(64 * ks * tpb));
     l.shmem = 0;
     return nullptr;
   }

@@ -15,7 +15,8 @@ namespace {
 // ---------------------------------------------------------------- rmsnorm
 // y = x / sqrt(mean(x * x) + eps) * w   (llama.py _rms_norm)
 // p[0] x, p[1] w, p[2] out; n[0] rows, n[1] D, n[2] x row stride, n[3] dtype,
-// n[4] weight dtype; f[0] eps.  One 256-thread block per row.
+// n[4] weight dtype, n[5] x and w start on 16-byte boundaries; f[0] eps.
+// One 256-thread block per row.
 __global__ __launch_bounds__(256) void k_rmsnorm(KArgs a) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -38,9 +39,68 @@ __global__ __launch_bounds__(256) void k_rmsnorm(KArgs a) {
   }
 }
 
+// The same rounding points for 16-bit rows of at most 8192 elements in
+// 16-byte vectors: each thread keeps its vectors of the row in registers
+// between the sum of squares and the normalisation (one pass over x), and
+// the dtype is a template parameter instead of a per-element switch.
+template <typename T, int VPT>
+__global__ __launch_bounds__(256) void k_rmsnorm_vec(KArgs a) {
+  using E = Elem<T>;
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t D = a.n[1], nv = D / 8;
+  const uint4* x = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[0]) + row * a.n[2]);
+  const uint4* w = static_cast<const uint4*>(a.p[1]);
+  uint4* out = reinterpret_cast<uint4*>(static_cast<T*>(a.p[2]) + row * D);
+  uint4 xv[VPT], wv[VPT];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const int64_t v = threadIdx.x + 256 * u;
+    xv[u] = v < nv ? x[v] : make_uint4(0, 0, 0, 0);
+    wv[u] = v < nv ? w[v] : make_uint4(0, 0, 0, 0);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    float f[8];
+    unpack<T>(xv[u], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += E::round(f[e] * f[e]);
+  }
+  ss = E::round(block_sum256(ss, red));
+  const float mean = E::round(ss / E::round(static_cast<float>(D)));
+  const float r = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const int64_t v = threadIdx.x + 256 * u;
+    if (v >= nv) break;
+    float f[8], g[8];
+    unpack<T>(xv[u], f);
+    unpack<T>(wv[u], g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = E::round(E::round(f[e] / r) * g[e]);
+    out[v] = pack<T>(f);
+  }
+}
+
+template <typename T>
+const void* pick_rmsnorm_vec(int64_t vectors) {
+  if (vectors <= 256) return reinterpret_cast<const void*>(&k_rmsnorm_vec<T, 1>);
+  if (vectors <= 512) return reinterpret_cast<const void*>(&k_rmsnorm_vec<T, 2>);
+  return reinterpret_cast<const void*>(&k_rmsnorm_vec<T, 4>);
+}
+
 const char* plan_rmsnorm(KArgs& a, Launch& l) {
   if (a.n[0] < 0 || a.n[1] <= 0) return "rmsnorm: bad sizes";
   if (a.n[0] > 2147483647) return "rmsnorm: too many rows";
+  const int dt = static_cast<int>(a.n[3]);
+  if ((dt == F16 || dt == BF16) && a.n[4] == dt && a.n[1] % 8 == 0 && a.n[1] <= 8192 && a.n[2] % 8 == 0 &&
+      a.n[5] != 0) {
+    l.func = dt == F16 ? pick_rmsnorm_vec<__half>(a.n[1] / 8) : pick_rmsnorm_vec<bf16_t>(a.n[1] / 8);
+    l.grid = dim3(static_cast<unsigned>(a.n[0] > 0 ? a.n[0] : 1));
+    l.block = dim3(256);
+    return nullptr;
+  }
   l.func = reinterpret_cast<const void*>(&k_rmsnorm);
   l.grid = dim3(static_cast<unsigned>(a.n[0] > 0 ? a.n[0] : 1));
   l.block = dim3(256);

@@ -444,8 +444,11 @@ def s_decode_attn(mem, p, n, f):
     qs, ks, vs = n[5:8], n[8:11], n[11:14]
     mode, length = n[14], n[15]
     cs = n[16:20]
-    wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes = n[20:29]
-    assert passes in (1, 2, 4)
+    wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes, stream_rows, unroll = n[20:31]
+    assert passes in (1, 2, 4) or (passes == 0 and stream_rows > 0 and unroll in (2, 4))
+    rpp = 16 if dt == 0 else 32
+    chunks = -(-C // stream_rows) if passes == 0 else -(-C // (rpp * passes))
+    assert chunks <= 64 and (passes != 0 or stream_rows % rpp == 0)
     G = H // KV
     div = _round(np.float32(f[0]), dt)
     error = 0

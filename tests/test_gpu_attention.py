@@ -24,13 +24,20 @@ def as_float(values):
     return bf16_to_float32(values) if values.dtype == BFLOAT16 else values.astype(np.float32)
 
 
-@pytest.mark.parametrize("passes", [0, 1, 4])
+@pytest.mark.parametrize("passes", [0, 1, 4, "stream8", "stream768"])
 @pytest.mark.parametrize("case", attention_cases.CASES, ids=lambda c: c.name)
 def test_decode_attention_matches_oracle(hip, case, passes, monkeypatch):
+    """passes: the chunk kernel's passes per workgroup (0 = chosen), or the
+    streaming kernel aiming at 8 workgroups (one range per KV head, many
+    tiles) or 768 (many short ranges, combined)."""
     from chomikgrad import _planner
 
     print(f"[gpu case] decode attention {case.name} passes={passes}", flush=True)
-    monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", passes)
+    if isinstance(passes, str):
+        monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", -1)
+        monkeypatch.setattr(_planner, "DECODE_ATTN_STREAM_WGS", int(passes[len("stream"):]))
+    else:
+        monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", passes)
     outputs, dynamic, caches = attention_cases.build(case)
     expected = realize(*outputs, compiler="cpu")
     tolerance = attention_cases.tolerance(case)

@@ -266,11 +266,12 @@ def test_memory_plan_reuses_the_arena():
     assert planned.arena_bytes <= 3 * per_value
 
 
-@pytest.mark.parametrize("passes", [0, 1, 2, 4])
+@pytest.mark.parametrize("passes", [0, 1, 2, 4, -1])
 @pytest.mark.parametrize("case", [c for c in attention_cases.CASES if c.C * c.B <= 1000], ids=lambda c: c.name)
 def test_decode_attention_fusion_matches_oracle(case, passes, monkeypatch):
     """The fused decode attention (split over cache chunks, combined by the
-    last workgroup) against the portable chain on the oracle; caches exact."""
+    last workgroup; -1 = the streaming kernel) against the portable chain on
+    the oracle; caches exact."""
     from chomikgrad import _planner
 
     monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", passes)
@@ -282,3 +283,26 @@ def test_decode_attention_fusion_matches_oracle(case, passes, monkeypatch):
         np.testing.assert_allclose(as_float(got[0]), as_float(expected[0]), **attention_cases.tolerance(case))
         for value, reference in zip(got[1:], expected[1:]):
             np.testing.assert_array_equal(np.asarray(value).view(np.uint8), np.asarray(reference).view(np.uint8))
+
+
+@pytest.mark.parametrize("B,KV,C,G,itemsize", [
+    (1, 4, 640, 8, 2), (8, 8, 4109, 4, 2), (1, 4, 32768, 8, 2), (2, 2, 70, 2, 4), (1, 1, 1, 1, 2)])
+def test_decode_attention_plan_limits(B, KV, C, G, itemsize, monkeypatch):
+    """Every plan covers the cache within the combine's 64 ranges per KV
+    head; the streaming ranges are whole passes; long caches stream."""
+    from chomikgrad import _planner
+
+    for forced in (0, -1, 1, 4):
+        monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", forced)
+        plan = _planner.decode_attention_plan(B, KV, C, G, itemsize)
+        rpp = _planner.decode_attention_rows(itemsize)
+        if plan["passes"] == 0:
+            assert plan["rows"] % rpp == 0 and plan["unroll"] in (2, 4)
+            assert plan["chunks"] == -(-C // plan["rows"])
+            assert (plan["chunks"] - 1) * plan["rows"] < C
+        else:
+            assert plan["chunks"] == -(-C // (rpp * plan["passes"]))
+        if forced == 0 and C >= 4096:
+            assert plan["passes"] == 0  # long caches always stream
+        if forced <= 0:
+            assert plan["chunks"] <= _planner.DECODE_ATTN_MAX_CHUNKS

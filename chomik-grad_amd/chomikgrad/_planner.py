@@ -1030,13 +1030,14 @@ def decode_attention_plan(B: int, KV: int, C: int, G: int, itemsize: int, diviso
     streaming kernel, whose ``chunks`` workgroups per KV head each stream
     ``rows`` cache rows in tiles of ``unroll`` passes."""
     rpp = decode_attention_rows(itemsize)
+    pow2 = divisor > 0 and math.frexp(divisor)[0] == 0.5
     stream = DECODE_ATTN_PASSES == -1
     if DECODE_ATTN_PASSES == 0:
         biggest = -(-C // (rpp * 4))
         stream = B * KV * biggest > DECODE_ATTN_STREAM_ABOVE or biggest > DECODE_ATTN_MAX_CHUNKS
     # the streaming kernel multiplies by the reciprocal of the score divisor,
     # exact only for a power of two (the usual sqrt(64) = 8)
-    stream = stream and divisor > 0 and math.frexp(divisor)[0] == 0.5
+    stream = stream and pow2
     if not stream:
         passes = decode_attention_passes(B, KV, C, itemsize)
         return {"passes": passes, "chunks": -(-C // (rpp * passes)), "rows": 0, "unroll": 0}

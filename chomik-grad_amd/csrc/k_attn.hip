@@ -73,9 +73,12 @@ __device__ __forceinline__ float reduce_scatter(float (&d)[G], int p) {
 #pragma unroll
       for (int i = 0; i < G / 2; ++i) {
         if (i < half) {
-          const float send = upper ? d[i] : d[i + half];
-          const float keep = upper ? d[i + half] : d[i];
-          d[i] = keep + __shfl_xor(send, o, 64);
+          float lo = d[i], hi = d[i + half];
+          // Opaque copies: a select between two elements of d would be
+          // folded into a runtime-indexed access of the whole array (a
+          // chain of G selects per element).
+          asm volatile("" : "+v"(lo), "+v"(hi));
+          d[i] = (upper ? hi : lo) + __shfl_xor(upper ? lo : hi, o, 64);
         }
       }
       held = half;

@@ -28,8 +28,8 @@ def as_float(values):
 @pytest.mark.parametrize("case", attention_cases.CASES, ids=lambda c: c.name)
 def test_decode_attention_matches_oracle(hip, case, passes, monkeypatch):
     """passes: the chunk kernel's passes per workgroup (0 = chosen), or the
-    streaming kernel aiming at 8 workgroups (one range per KV head, many
-    tiles) or 768 (many short ranges, combined)."""
+    streaming kernel aiming at 8 workgroups (one or two ranges per KV head,
+    many tiles) or 768 (many short ranges, combined)."""
     from chomikgrad import _planner
 
     print(f"[gpu case] decode attention {case.name} passes={passes}", flush=True)

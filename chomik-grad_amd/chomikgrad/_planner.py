@@ -178,6 +178,8 @@ class Step:
                 values.append(segment["w"])
                 if segment["res"] is not None:
                     values.append(segment["res"])
+            if self.attrs.get("workspace") is not None:  # split MFMA GEMV: tickets and partials
+                values.append(self.attrs["workspace"])
             return values
         return [pv for pv in self.ins if pv is not None]
 
@@ -573,10 +575,17 @@ class Emitter:
         if self._is_placement(a, b, node):
             # A @ eye(S, C): A's columns in the first S output columns, zeros
             # after them (the prefill KV-cache placement, llama.py
-            # LlamaForCausalLM.prefill)
-            out = self.new_value(node.shape, node.dtype, "placement")
-            self.add(K_FILL, [], [out], words=(out.size * out.itemsize + 3) // 4)
-            view = PV(a.shape, node.dtype, out.strides[:-1] + (1,), out.storage, out.offset)
+            # LlamaForCausalLM.prefill: (K^T @ eye(S, C))^T).  The result is
+            # stored with its last two axes swapped -- the (C, D) layout of
+            # the cache the graph transposes it back into -- so that
+            # transpose is a view and the placement one row-contiguous copy.
+            shape = tuple(node.shape)
+            swapped = shape[:-2] + (shape[-1], shape[-2])
+            dense = self.new_value(swapped, node.dtype, "placement")
+            strides = dense.strides[:-2] + (dense.strides[-1], dense.strides[-2])
+            out = PV(shape, node.dtype, strides, dense.storage, dense.offset)
+            self.add(K_FILL, [], [dense], words=(dense.size * dense.itemsize + 3) // 4)
+            view = PV(a.shape, node.dtype, strides, dense.storage, dense.offset)
             self.add(K_COPY, [a], [view])
             return out
         return self.matmul(node, a, b)
@@ -716,7 +725,11 @@ class Emitter:
 
     def lower_sdpa(self, node, args, scale):
         q, k, v, mask = args
-        out = self.new_value(node.shape, node.dtype, "sdpa")
+        # (B, H, T, hd) stored as (B, T, H, hd): the graph transposes the
+        # heads back next to each other before o_proj, which is then a view
+        B, H, T, hd = node.shape
+        dense = self.new_value((B, T, H, hd), node.dtype, "sdpa")
+        out = PV(tuple(node.shape), node.dtype, (T * H * hd, hd, H * hd, 1), dense.storage, dense.offset)
         if out.size:
             causal = self._causal_mask_value(mask, q.shape[2], k.shape[2], q.dtype)
             self.add(K_SDPA, [q, k, v, mask], [out], divisor=float(1.0 / float(scale)),
@@ -822,6 +835,60 @@ def mfma_gemv(step: Step) -> bool:
     x = step.ins[0]
     return (2 <= step.attrs["rows"] <= 16 and x.itemsize == 2 and step.attrs["K"] % 32 == 0
             and all(seg["w"].shape[0] % 16 == 0 for seg in step.attrs["segments"]))
+
+
+GEMV_MFMA_BLOCKS = int(os.environ.get("CHOMIK_HIP_GEMV_MFMA_BLOCKS", "512"))
+GEMV_MFMA_BLOCK_KSTEPS = int(os.environ.get("CHOMIK_HIP_GEMV_MFMA_BLOCK_KSTEPS", "64"))
+
+
+def mfma_gemv_blocks(step: Step) -> int:
+    """Blocks that share one 16-column tile of an MFMA GEMV, each over an
+    equal share of K: doubled while the launch has fewer than
+    GEMV_MFMA_BLOCKS blocks and each block keeps at least
+    GEMV_MFMA_BLOCK_KSTEPS k-steps of 32.  Narrow matrices over a long K
+    (2048 columns over K = 8192: 17.4 -> 13.9 us at batch 8) otherwise occupy
+    only half of the CUs; below 64 k-steps per block (K = 2048 split four
+    ways) the partial exchange costs more than the CUs gain."""
+    if not mfma_gemv(step) or step.attrs["prologue"] is not None:
+        return 1
+    segments = step.attrs["segments"]
+    cols = segments[0]["w"].shape[0] if step.attrs["silu"] else sum(seg["w"].shape[0] for seg in segments)
+    tiles, ksteps = cols // 16, step.attrs["K"] // 32
+    kb = 1
+    while (tiles * kb < GEMV_MFMA_BLOCKS and ksteps % (kb * 8) == 0
+           and ksteps // (kb * 2) >= max(16, GEMV_MFMA_BLOCK_KSTEPS)):
+        kb *= 2
+    return kb
+
+
+def _gemv_tiles(step: Step) -> int:
+    segments = step.attrs["segments"]
+    cols = segments[0]["w"].shape[0] if step.attrs["silu"] else sum(seg["w"].shape[0] for seg in segments)
+    return cols // 16
+
+
+def gemv_partial_bytes(step: Step, kb: int) -> int:
+    """Partial tiles of a split MFMA GEMV: kb 16x16 float32 tiles per column
+    tile and B operand."""
+    return _gemv_tiles(step) * kb * (2 if step.attrs["silu"] else 1) * 256 * 4
+
+
+def attach_gemv_workspace(steps: List[Step], emitter: "Emitter") -> List[Step]:
+    """Gives every MFMA GEMV split over blocks one shared, zero-initialised
+    workspace (p[14]): a ticket region of one int32 per tile of the widest
+    such GEMV (256-byte aligned, n[25] bytes, always back at zero after a
+    launch: the tickets reset themselves), then the partial tiles of the
+    largest.  Steps run in order, so one buffer serves all of them."""
+    split = [(step, mfma_gemv_blocks(step)) for step in steps if step.kind == K_GEMV]
+    split = [(step, kb) for step, kb in split if kb > 1]
+    if not split:
+        return steps
+    ticket_bytes = -(-max(_gemv_tiles(step) for step, _ in split) * 4 // 256) * 256
+    partial_bytes = max(gemv_partial_bytes(step, kb) for step, kb in split)
+    workspace = emitter.zeros(ticket_bytes + partial_bytes, "gemv_workspace")
+    for step, kb in split:
+        step.attrs.update(blocks=kb, workspace=workspace, ticket_bytes=ticket_bytes)
+    return steps
 
 
 def fuse_rmsnorm_prologue(steps: List[Step], outputs: List[PV]) -> List[Step]:
@@ -1117,6 +1184,43 @@ def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitte
     return [s for s in steps if id(s) not in removed]
 
 
+GEMM_SEGMENT_WIDTH = 128  # segment widths of a merged GEMM: whole 128-column tiles
+
+
+def merge_sibling_gemms(steps: List[Step]) -> List[Step]:
+    """Plain GEMMs of the same A (the prefill q, k and v projections) -> one
+    launch with up to four output segments: one pass over A, and the narrow
+    k and v products (256 columns) no longer run as launches of their own."""
+    removed = set()
+    for i, first in enumerate(steps):
+        if first.kind != K_GEMM or id(first) in removed or first.attrs.get("res") is not None \
+                or first.attrs.get("up") is not None:
+            continue
+        group = [first]
+        for later in steps[i + 1:]:
+            if len(group) == 4:
+                break
+            if later.kind != K_GEMM or id(later) in removed or later.attrs.get("res") is not None \
+                    or later.attrs.get("up") is not None:
+                continue
+            if later.attrs["K"] != first.attrs["K"] or later.attrs["rows"] != first.attrs["rows"]:
+                continue
+            if not later.ins[0].same_data(first.ins[0]) or later.ins[0].dtype != first.ins[0].dtype:
+                continue
+            group.append(later)
+        widths = [s.attrs["N"] for s in group]
+        if len(group) < 2 or any(w % GEMM_SEGMENT_WIDTH for w in widths):
+            continue
+        if any(s.outs[0].row_stride() is None or s.ins[1].strides[-1] != 1 for s in group):
+            continue
+        first.attrs["segments"] = [(s.ins[1], s.outs[0]) for s in group]
+        first.attrs["N"] = sum(widths)
+        first.ins = [first.ins[0]] + [s.ins[1] for s in group]
+        first.outs = [s.outs[0] for s in group]
+        removed.update(id(s) for s in group[1:])
+    return [s for s in steps if id(s) not in removed]
+
+
 def merge_sibling_gemvs(steps: List[Step]) -> List[Step]:
     removed = set()
     for i, first in enumerate(steps):
@@ -1224,10 +1328,11 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         return kind, [_ptr(out)], [a["words"], 0], []
     if kind == K_COPY:
         src, dst = step.ins[0], step.outs[0]
-        strided = not dst.contiguous()
+        shape, src_strides, dst_strides = copy_order(src.shape, src.strides, dst.strides)
+        strided = dst_strides != contiguous_strides(shape)
         return kind, [_ptr(src), _ptr(dst)], (
-            [src.size, len(src.shape)] + _pad(src.shape, 8, 1) + _pad(src.strides, 8) + [src.itemsize]
-            + [1 if strided else 0] + _pad(dst.strides if strided else (), 8)
+            [src.size, len(shape)] + _pad(shape, 8, 1) + _pad(src_strides, 8) + [src.itemsize]
+            + [1 if strided else 0] + _pad(dst_strides if strided else (), 8)
         ), []
     if kind == K_ELEMENTWISE:
         out = step.outs[0]
@@ -1301,6 +1406,8 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         causal = a.get("causal")
         aligned = all(pv.offset % 8 == 0 for pv in (q, k, v))
         ints += [1 if causal is not None else 0, 1 if aligned else 0]
+        assert out.strides[3] == 1 or out.shape[3] == 1
+        ints += list(out.strides[:3])
         return kind, [_ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(out)], ints, [
             a["divisor"], causal if causal is not None else 0.0]
     if kind == K_KV_WRITE:
@@ -1344,10 +1451,17 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         x, w = step.ins[0], step.ins[1]
         out = step.outs[0]
         res, up = a.get("res"), a.get("up")
-        return kind, [_ptr(x), _ptr(w), _ptr(out), _ptr(res), _ptr(up)], [
-            a["rows"], a["N"], a["K"], dtype_code(x.dtype), x.row_stride(), w.strides[0], a["N"],
-            a["N"] if res is not None else 0, 1 if up is not None else 0,
-            up.strides[0] if up is not None else 0, 1 if res is not None else 0], []
+        segments = a.get("segments") or []  # [(w, out)] of merged siblings
+        ptrs = [_ptr(x), _ptr(w), _ptr(out), _ptr(res), _ptr(up)]
+        for sw, so in segments[1:]:
+            ptrs += [_ptr(sw), _ptr(so)]
+        ints = [a["rows"], a["N"], a["K"], dtype_code(x.dtype), x.row_stride(), w.strides[0],
+                out.row_stride() if segments else a["N"],
+                a["N"] if res is not None else 0, 1 if up is not None else 0,
+                up.strides[0] if up is not None else 0, 1 if res is not None else 0]
+        ints += [len(segments)] + _pad([sw.shape[0] for sw, _ in segments], 4)
+        ints += _pad([so.row_stride() for _, so in segments], 4) + _pad([sw.strides[0] for sw, _ in segments], 4)
+        return kind, ptrs, ints, []
     if kind == K_GEMV:
         segments = a["segments"]
         prologue = a["prologue"]
@@ -1356,6 +1470,7 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         ptrs += [_ptr(s["w"]) for s in segments] + [(-1, 0)] * (4 - len(segments))
         ptrs += [_ptr(s["out"]) for s in segments] + [(-1, 0)] * (4 - len(segments))
         ptrs += [_ptr(s["res"]) for s in segments] + [(-1, 0)] * (4 - len(segments))
+        ptrs += [_ptr(a.get("workspace"))]
         rows, K = a["rows"], a["K"]
         n = [s["w"].shape[0] for s in segments]
         stage = rows * K * x.itemsize <= GEMV_STAGE_BYTES
@@ -1370,9 +1485,29 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         vector = 16 // x.itemsize
         aligned = x.row_stride() % vector == 0 and (_ptr(x)[1] % 16) == 0
         ints += [dtype_code(prologue["w"].dtype) if prologue else 0, 1 if stage else 0, GEMV_SPLIT,
-                 1 if aligned else 0]
+                 1 if aligned else 0, 0, a.get("blocks", 1), a.get("ticket_bytes", 0)]
         return kind, ptrs, ints, [prologue["eps"] if prologue else 0.0]
     raise AssertionError(f"no encoder for step kind {kind}")
+
+
+def copy_order(shape: Sequence[int], src_strides: Sequence[int], dst_strides: Sequence[int]):
+    """The axes of an element copy in the order the kernel walks them: by
+    destination stride, largest first (the last axis the destination's
+    fastest), size-1 axes dropped and neighbours that are contiguous in both
+    source and destination merged.  A transposed pair of views (the prefill
+    KV placement) becomes a copy of contiguous rows."""
+    axes = [d for d in range(len(shape)) if shape[d] != 1]
+    axes.sort(key=lambda d: (-dst_strides[d], -src_strides[d]))
+    dims = [[shape[d], src_strides[d], dst_strides[d]] for d in axes]
+    merged: List[List[int]] = []
+    for size, ss, ds in dims:
+        if merged and merged[-1][1] == ss * size and merged[-1][2] == ds * size:
+            merged[-1] = [merged[-1][0] * size, ss, ds]
+        else:
+            merged.append([size, ss, ds])
+    if not merged:
+        merged = [[1, 1, 1]]
+    return (tuple(m[0] for m in merged), tuple(m[1] for m in merged), tuple(m[2] for m in merged))
 
 
 def build_tape(steps: List[Step], n_slots: int, arena_bytes: int) -> np.ndarray:
@@ -1435,7 +1570,9 @@ def plan_graph(compiler, outputs: Sequence[LazyNode], dynamic_inputs: Sequence[L
     steps = fuse_residual(steps, out_pvs)
     steps = fuse_gemm_epilogues(steps, out_pvs)
     steps = merge_sibling_gemvs(steps)
+    steps = merge_sibling_gemms(steps)
     steps = fuse_decode_attention(steps, out_pvs, emitter)
+    steps = attach_gemv_workspace(steps, emitter)
 
     # Program outputs: leaves are returned as they are, whole intermediates
     # become caller-visible buffers, anything else is copied into one.

@@ -174,6 +174,18 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Values exchanged between workgroups that may sit on different XCDs (each
+// with its own L2): agent-scope atomic stores and loads are coherent across
+// them without the whole-L2 writeback and invalidate that a device-scope
+// fence costs.  A writer waits for its stores to complete (s_waitcnt) before
+// it signals, e.g. by an agent-scope atomic ticket.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Sum over a 256-thread block (4 waves); every thread gets the result.
 __device__ __forceinline__ float block_sum256(float v, float* scratch4) {
   v = wave_sum(v);

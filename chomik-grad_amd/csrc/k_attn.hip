@@ -90,16 +90,8 @@ __device__ __forceinline__ float reduce_scatter(float (&d)[G], int p) {
 }
 
 // The partials are exchanged between workgroups that may sit on different
-// XCDs (each with its own L2).  Agent-scope atomic stores and loads are
-// coherent across them without the whole-L2 writeback and invalidate that a
-// device-scope fence costs; the writer waits for its stores to complete
-// before it takes a ticket.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// XCDs through store_agent / load_agent; the writer waits for its stores to
+// complete before it takes a ticket.
 
 // Called by every workgroup of (sequence b, KV head g) after it stored its
 // partials (P V sums, maximum and exp-sum per query head of the group): the

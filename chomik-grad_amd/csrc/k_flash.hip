@@ -54,12 +54,12 @@ template <> struct FlashMfma<bf16_t> {
 };
 
 // K_SDPA layout (shared with k_sdpa): p[0] q, p[1] K, p[2] V, p[3] mask (or
-// null), p[4] out (B, H, T, 64) contiguous.  n[0] B, n[1] H, n[2] T, n[3] C,
-// n[4] hd, n[5] KV, n[6] dtype, n[7..10] q strides (b, h, t, d), n[11..14]
-// K strides (b, kv, c, d), n[15..18] V strides, n[19..22] mask strides
-// (b, h, t, c), n[23] mask dtype, n[24] causal mask proved, n[25] q, K, V
-// views start on 16-byte boundaries; f[0] d, f[1] the causal mask's value
-// above the diagonal.
+// null), p[4] out (B, H, T, 64).  n[0] B, n[1] H, n[2] T, n[3] C, n[4] hd,
+// n[5] KV, n[6] dtype, n[7..10] q strides (b, h, t, d), n[11..14] K strides
+// (b, kv, c, d), n[15..18] V strides, n[19..22] mask strides (b, h, t, c),
+// n[23] mask dtype, n[24] causal mask proved, n[25] q, K, V views start on
+// 16-byte boundaries, n[26..28] out strides (b, h, t; unit along hd);
+// f[0] d, f[1] the causal mask's value above the diagonal.
 template <typename T>
 __global__ __launch_bounds__(256) void k_flash_prefill(KArgs a) {
   using E = Elem<T>;
@@ -209,14 +209,15 @@ __global__ __launch_bounds__(256) void k_flash_prefill(KArgs a) {
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
 
-  T* out = static_cast<T*>(a.p[4]) + (b * H + h) * Tq * kD;
+  T* out = static_cast<T*>(a.p[4]) + b * a.n[26] + h * a.n[27];
+  const int64_t ot = a.n[28];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const float inv = 1.0f / __shfl(lsum, 4 * fg + r, 64);
     const int64_t q = q0 + 16 * w + 4 * fg + r;
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn)
-      if (q < Tq) out[q * kD + 16 * tn + fi] = E::from_f(o[tn][r] * inv);
+      if (q < Tq) out[q * ot + 16 * tn + fi] = E::from_f(o[tn][r] * inv);
   }
 }
 

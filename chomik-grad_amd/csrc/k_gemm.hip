@@ -48,11 +48,15 @@ template <> struct Mfma<bf16_t> {
 };
 
 // p[0] A, p[1] W (the gate weight with SILU), p[2] C, p[3] residual R (or
-// null), p[4] the up weight (SILU).
+// null), p[4] the up weight (SILU); p[5..10] the W and C of output segments
+// 1..3.
 // n[0] M, n[1] N, n[2] K, n[3] dtype, n[4] lda, n[5] ldw, n[6] ldc,
 // n[7] ldr, n[8] SiLU epilogue, n[9] ldw of the up weight, n[10] residual
 // epilogue (elements; the planner picks the kernel from these flags, the
-// pointers are bound later).
+// pointers are bound later), n[11] output segments (0 or 1: one), n[12..15]
+// their widths (multiples of 128: a tile lies in one segment), n[16..19]
+// their ldc, n[20..23] their ldw.  Segments are sibling products of the
+// same A (q, k and v projections) in one launch; plain epilogue only.
 // Epilogues (the portable graph's rounding points, as in the decode GEMVs):
 //  * RES:  C = round(R + round(acc))
 //  * SILU: the tile's weight rows alternate, 16 at a time, between the gate
@@ -70,8 +74,9 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
   __shared__ __attribute__((aligned(16))) T As[2][BM * kRow];
   __shared__ __attribute__((aligned(16))) T Ws[2][BN * kRow];
 
-  const int64_t M = a.n[0], N = a.n[1], K = a.n[2];
-  const int64_t lda = a.n[4], ldw = a.n[5], ldc = a.n[6];
+  const int64_t M = a.n[0], K = a.n[2];
+  const int64_t lda = a.n[4];
+  int64_t N = a.n[1], ldw = a.n[5], ldc = a.n[6];
   const T* A = static_cast<const T*>(a.p[0]);
   const T* W = static_cast<const T*>(a.p[1]);
   T* C = static_cast<T*>(a.p[2]);
@@ -84,7 +89,18 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
   const int64_t per_xcd = (tiles + 7) / 8;
   const int64_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (tile >= tiles) return;  // whole block: no barrier is skipped by part of it
-  const int64_t m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * ON;
+  const int64_t m0 = (tile / tiles_n) * BM;
+  int64_t n0 = (tile % tiles_n) * ON;
+  if (!SILU && !RES && a.n[11] > 1) {  // this tile's output segment (uniform selects)
+    const int64_t w0 = a.n[12], w1 = a.n[13], w2 = a.n[14];
+    const int seg = n0 < w0 ? 0 : n0 < w0 + w1 ? 1 : n0 < w0 + w1 + w2 ? 2 : 3;
+    n0 -= seg == 0 ? 0 : seg == 1 ? w0 : seg == 2 ? w0 + w1 : w0 + w1 + w2;
+    N = seg == 0 ? w0 : seg == 1 ? w1 : seg == 2 ? w2 : a.n[15];
+    ldc = seg == 0 ? a.n[16] : seg == 1 ? a.n[17] : seg == 2 ? a.n[18] : a.n[19];
+    ldw = seg == 0 ? a.n[20] : seg == 1 ? a.n[21] : seg == 2 ? a.n[22] : a.n[23];
+    W = static_cast<const T*>(seg == 0 ? a.p[1] : seg == 1 ? a.p[5] : seg == 2 ? a.p[7] : a.p[9]);
+    C = static_cast<T*>(seg == 0 ? a.p[2] : seg == 1 ? a.p[6] : seg == 2 ? a.p[8] : a.p[10]);
+  }
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -212,10 +228,21 @@ const char* plan_gemm(KArgs& a, Launch& l) {
   if (M <= 0 || N <= 0 || K <= 0) return "gemm: empty operands";
   if (dt != F16 && dt != BF16) return "gemm: float16 or bfloat16 operands required";
   if (K % 8 || a.n[4] % 8 || a.n[5] % 8) return "gemm: k and row strides must be multiples of 8 elements";
-  if (a.n[4] < K || a.n[5] < K || a.n[6] < N) return "gemm: row stride shorter than the row";
+  if (a.n[4] < K || a.n[5] < K || (a.n[11] <= 1 && a.n[6] < N)) return "gemm: row stride shorter than the row";
   const bool silu = a.n[8] != 0, res = a.n[10] != 0;
   if (silu && (res || a.n[9] % 8 || a.n[9] < K)) return "gemm: bad SiLU operands";
   if (res && a.n[7] < N) return "gemm: residual row stride shorter than the row";
+  if (a.n[11] > 1) {
+    if (a.n[11] > 4 || silu || res) return "gemm: 2..4 output segments, plain epilogue only";
+    int64_t total = 0;
+    for (int s = 0; s < a.n[11]; ++s) {
+      const int64_t w = a.n[12 + s];
+      if (w <= 0 || w % 128 || a.n[16 + s] < w || a.n[20 + s] < K || a.n[20 + s] % 8)
+        return "gemm: segments must be multiples of 128 columns with full rows";
+      total += w;
+    }
+    if (total != N) return "gemm: segment widths must add up to N";
+  }
   // 128 x 128 tiles once they fill the chip twice over, else 64 x 64 (output
   // tiles are half as wide with the SiLU pair)
   const int64_t span = silu ? 2 : 1;

@@ -976,7 +976,10 @@ __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int fi = lane & 15, fg = lane >> 4;
   const int kp = w % KS;
-  const int64_t tile = blockIdx.x * int64_t(TPB) + w / KS;
+  // n[24] > 1: KB consecutive blocks share a column tile, each over K / KB
+  const int64_t KB = a.n[24] > 1 ? a.n[24] : 1;
+  const int64_t kb = blockIdx.x % KB;
+  const int64_t tile = (blockIdx.x / KB) * int64_t(TPB) + w / KS;
   const bool tile_ok = tile * 16 < cols;
   const int64_t n0 = tile_ok ? tile * 16 : 0;  // out-of-range tiles compute tile 0 and store nothing
 
@@ -998,8 +1001,8 @@ __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) 
   const uint4 zero = make_uint4(0, 0, 0, 0);
 
   const int64_t kv = K / 8;                 // 16-byte vectors per row
-  const int64_t steps = K / 32 / KS;        // k-steps of this wave
-  const int64_t v0 = kp * steps * 4;        // first vector of this wave's k range
+  const int64_t steps = K / 32 / KB / KS;   // k-steps of this wave
+  const int64_t v0 = (kb * KS + kp) * steps * 4;  // first vector of this wave's k range
   const int64_t vend = v0 + steps * 4;
   uint4 xa[2][kChunk], wb[2][NB][kChunk];
   auto issue = [&](int buf, int64_t c) {
@@ -1050,6 +1053,40 @@ __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) 
     }
   }
   if (kp != 0 || !tile_ok) return;
+
+  // Split over blocks: every block stores its partial tile (p[14]: one
+  // ticket per tile in the first n[25] bytes, then the partials); the last
+  // block of the tile to arrive -- a self-resetting ticket, no spinning --
+  // adds the KB partials in block order (the same sum whatever the arrival
+  // order) and finishes.
+  if (KB > 1) {
+    if (a.p[14] == nullptr) {  // a workspace is required (planned with it)
+      if (lane == 0) raise_error(a, ERR_SHAPE);
+      return;
+    }
+    int* tickets = static_cast<int*>(a.p[14]);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(a.p[14]) + a.n[25]);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) store_agent(part + ((tile * KB + kb) * NB + b) * 256 + r * 64 + lane, acc[b][r]);
+    __builtin_amdgcn_s_waitcnt(0);  // the partial is stored before the ticket is taken
+    int last = 0;
+    if (lane == 0) {
+      const int ticket = __hip_atomic_fetch_add(&tickets[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = ticket == static_cast<int>(KB) - 1;
+      if (last) __hip_atomic_store(&tickets[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      mf4v sum = mf4v{0.f, 0.f, 0.f, 0.f};
+      for (int64_t q = 0; q < KB; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[r] += load_agent(part + ((tile * KB + q) * NB + b) * 256 + r * 64 + lane);
+      acc[b] = sum;
+    }
+  }
 
   // lane (fi, fg) holds D[4 fg + r][fi]: input row 4 fg + r, column n0 + fi
 #pragma unroll
@@ -1165,19 +1202,25 @@ const char* plan_gemv(KArgs& a, Launch& l) {
       a.n[2] % 8 == 0 && aligned) {
     const int64_t cols = silu ? a.n[7] : rows;
     const int64_t tiles = cols / 16;
-    // Split K over up to 16 waves of a block while the launch has fewer
-    // than 2048 waves and each wave keeps at least one register chunk.
+    // n[24]: blocks sharing a column tile over K (chosen with the workspace
+    // in p[14]); then split each block's K over up to 16 waves while the
+    // launch has fewer than 2048 waves and each wave keeps at least one
+    // register chunk.
+    const int64_t kbs = a.n[24] > 1 ? a.n[24] : 1;
+    if ((K / 32) % kbs) return "gemv: K must split evenly over the blocks of a tile";
+    if (kbs > 1 && (a.n[25] < tiles * 4 || a.n[25] % 256)) return "gemv: the ticket region must hold one ticket per tile";
     static const int max_ks = env_int("CHOMIK_HIP_GEMV_MFMA_SPLIT", 16);
-    const int64_t ksteps = K / 32;
+    const int64_t ksteps = K / 32 / kbs;
     int ks = 1;
-    while (ks < max_ks && ks < 16 && tiles * ks < 2048 && ksteps % (ks * 2) == 0 && ksteps / (ks * 2) >= kChunk)
+    while (ks < max_ks && ks < 16 && tiles * kbs * ks < 2048 && ksteps % (ks * 2) == 0 && ksteps / (ks * 2) >= kChunk)
       ks *= 2;
     const int64_t tpb = ks >= 4 ? 1 : 4 / ks;
-    const int64_t blocks = (tiles + tpb - 1) / tpb;
+    const int64_t blocks = (tiles + tpb - 1) / tpb * kbs;
     if (blocks > 2147483647) return "gemv: too many rows";
     l.func = dt == F16 ? pick_mfma<__half>(ks, silu) : pick_mfma<bf16_t>(ks, silu);
     l.grid = dim3(static_cast<unsigned>(blocks));
     l.block = dim3(static_cast<unsigned>(64 * ks * tpb));
+    a.p[kErrPtr] = device_error_word();
     l.shmem = 0;
     return nullptr;
   }

@@ -167,7 +167,8 @@ const char* plan_rope(KArgs& a, Launch& l) {
 // p[0] q, p[1] K, p[2] V, p[3] mask (or null), p[4] out (B, H, T, hd).
 // n[0] B, n[1] H, n[2] T, n[3] C, n[4] hd, n[5] KV, n[6] dtype, n[7..10] q
 // strides (b, h, t, d), n[11..14] K strides (b, kv, c, d), n[15..18] V
-// strides, n[19..22] mask strides (b, h, t, c), n[23] mask dtype; f[0] d.
+// strides, n[19..22] mask strides (b, h, t, c), n[23] mask dtype, n[26..28]
+// out strides (b, h, t; unit stride along hd); f[0] d.
 // One 256-thread block per (b, h, t); scores live in dynamic LDS.
 __global__ __launch_bounds__(256) void k_sdpa(KArgs a) {
   extern __shared__ float lds[];
@@ -218,7 +219,7 @@ __global__ __launch_bounds__(256) void k_sdpa(KArgs a) {
     __syncthreads();
     if (group == 0 && d < hd) {
       const float total = (partial[lane] + partial[64 + lane]) + (partial[128 + lane] + partial[192 + lane]);
-      store_f(a.p[4], row * hd + d, dt, total);
+      store_f(a.p[4], b * a.n[26] + h * a.n[27] + t * a.n[28] + d, dt, total);
     }
   }
 }

@@ -338,7 +338,10 @@ def s_sdpa(mem, p, n, f):
                     e = _round(np.exp(_round(s - s.max(), dt)), dt)
                     S = _round(e.sum(), dt)
                     out[b, h, t] = (_round(e / S, dt).astype(np.float64) @ V).astype(np.float32)
-    store(mem, p[4], dt, np.arange(out.size), out.reshape(-1))
+    o = n[26:29]
+    index = (np.arange(B)[:, None, None, None] * o[0] + np.arange(H)[None, :, None, None] * o[1]
+             + np.arange(T)[None, None, :, None] * o[2] + np.arange(hd)[None, None, None, :])
+    store(mem, p[4], dt, index.reshape(-1), out.reshape(-1))
     return 0
 
 
@@ -395,6 +398,8 @@ def s_kv_place(mem, p, n, f):
 
 def s_gemv(mem, p, n, f):
     M, K, xs, dt, nseg, pro, silu = n[0:7]
+    # a GEMV split over blocks needs its bound workspace (tickets, partials)
+    assert n[24] <= 1 or (p[14][0] >= 0 and n[25] >= 4 * -(-max(n[7:11]) // 16)), "split GEMV without a workspace"
     Ns = n[7:11]
     ostr = n[11:15]
     rstr = n[15:19]
@@ -424,6 +429,17 @@ def s_gemv(mem, p, n, f):
 def s_gemm(mem, p, n, f):
     M, N, K, dt, lda, ldw, ldc, ldr, silu, ldwu, has_res = n[0:11]
     A = load(mem, p[0], dt, np.arange(M)[:, None] * lda + np.arange(K)[None, :])
+    if n[11] > 1:  # output segments: sibling products of A
+        assert not silu and not has_res and sum(n[12:12 + n[11]]) == N
+        wp = [p[1]] + [p[5 + 2 * k] for k in range(n[11] - 1)]
+        cp = [p[2]] + [p[6 + 2 * k] for k in range(n[11] - 1)]
+        for s in range(n[11]):
+            Ns, lc, lw = n[12 + s], n[16 + s], n[20 + s]
+            assert Ns % 128 == 0
+            W = load(mem, wp[s], dt, np.arange(Ns)[:, None] * lw + np.arange(K)[None, :])
+            C = _round((A.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32), dt)
+            store(mem, cp[s], dt, (np.arange(M)[:, None] * lc + np.arange(Ns)[None, :]).reshape(-1), C.reshape(-1))
+        return 0
     W = load(mem, p[1], dt, np.arange(N)[:, None] * ldw + np.arange(K)[None, :])
     C = _round((A.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32), dt)
     if silu:  # C = round(silu(round(g)) * round(u)), silu(g) = round(g / round(round(exp(-g)) + 1))

@@ -154,6 +154,40 @@ def test_gemv_linear_variants(hip, dtype, rows):
 
 
 @pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("rows", [2, 8])
+@pytest.mark.parametrize("K,N", [(8192, 384), (4096, 256)], ids=["k8192", "k4096"])
+def test_gemv_split_over_blocks(hip, dtype, rows, K, N):
+    """MFMA GEMVs whose column tiles are shared by several blocks (each over
+    a share of K, the last block to finish adds the partials in block order):
+    plain, residual and SiLU-pair epilogues and a narrower GEMV sharing the
+    workspace, against the oracle; a second run (tickets reset) is
+    bit-identical."""
+    from chomikgrad import _planner
+
+    announce(f"gemv split {np.dtype(dtype)} rows={rows} K={K} N={N}")
+    rng = np.random.default_rng(K + rows)
+    x = Tensor(rng.normal(size=(1, rows, K)).astype(np.float32), dtype=dtype)
+    h = Tensor(rng.normal(size=(1, rows, N)).astype(np.float32), dtype=dtype)
+    w1 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
+    w2 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
+    # a GEMV of another width on its own input shares the workspace
+    z = Tensor(rng.normal(size=(1, rows, K)).astype(np.float32), dtype=dtype)
+    w3 = Tensor((rng.normal(size=(160, K)) * 0.05).astype(np.float32), dtype=dtype)
+    gate = x @ w1.T
+    outputs = [x @ w2.T, h + (x @ w1.T), gate / (1 + (-gate).exp()) * (x @ w2.T), z @ w3.T]
+    program = compile_graph(*outputs, compiler="hip")
+    gemvs = [s for s in program._planned.steps if s.kind == _planner.K_GEMV]
+    assert gemvs and all(s.attrs.get("blocks", 1) > 1 for s in gemvs)
+    got = program()
+    expected = realize(*outputs, compiler="cpu")
+    for g, e in zip(got, expected):
+        np.testing.assert_allclose(as_float(g), as_float(e), rtol=3e-2, atol=3e-2)
+    again = program()
+    for g, a in zip(got, again):
+        np.testing.assert_array_equal(np.asarray(g).view(np.uint8), np.asarray(a).view(np.uint8))
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("shape", [(37, 200, 72), (130, 96, 512), (9, 4100, 264), (2048, 4096, 256)],
                          ids=["ragged", "tall", "wide", "large-tiles"])
 def test_gemm_linear_matches_fp32_reference(hip, dtype, shape):

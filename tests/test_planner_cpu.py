@@ -176,7 +176,8 @@ def test_half_precision_prefill_uses_mfma_gemm(dtype):
     expected = realize(*outputs, compiler="cpu")
     planned, got = model_run(outputs, [tokens])
     gemms = [s for s in planned.steps if s.kind == K_GEMM]
-    assert len(gemms) == 6  # q, k, v, o (+ residual), gate/up (+ SiLU), down (+ residual)
+    assert len(gemms) == 4  # q|k|v (one launch), o (+ residual), gate/up (+ SiLU), down (+ residual)
+    assert sum(len(g.attrs.get("segments") or ()) == 3 for g in gemms) == 1
     assert sum(g.attrs.get("up") is not None for g in gemms) == 1
     assert sum(g.attrs.get("res") is not None for g in gemms) == 2
     assert not any(s.kind == K_ELEMENTWISE for s in planned.steps)
@@ -306,3 +307,31 @@ def test_decode_attention_plan_limits(B, KV, C, G, itemsize, monkeypatch):
             assert plan["passes"] == 0  # long caches always stream
         if forced <= 0:
             assert plan["chunks"] <= _planner.DECODE_ATTN_MAX_CHUNKS
+
+
+def test_mfma_gemv_block_split_plan():
+    """Narrow MFMA GEMVs share each 16-column tile among several blocks over
+    K, with one zero-initialised workspace (tickets, then the partial tiles)
+    sized for the largest; wide or short-K ones stay unsplit; the planned
+    program computes the portable chain's values."""
+    from chomikgrad import _planner
+
+    rng = np.random.default_rng(3)
+    x = Tensor(rng.normal(size=(1, 8, 8192)).astype(np.float32), dtype=np.float16)
+    h = Tensor(rng.normal(size=(1, 8, 384)).astype(np.float32), dtype=np.float16)
+    narrow = Tensor((rng.normal(size=(384, 8192)) * 0.02).astype(np.float32), dtype=np.float16)
+    wide = Tensor((rng.normal(size=(8192, 2048)) * 0.05).astype(np.float32), dtype=np.float16)
+    short = Tensor((rng.normal(size=(384, 256)) * 0.05).astype(np.float32), dtype=np.float16)
+    y = Tensor(rng.normal(size=(1, 8, 256)).astype(np.float32), dtype=np.float16)
+    z = Tensor(rng.normal(size=(1, 8, 2048)).astype(np.float32), dtype=np.float16)
+    outputs = [h + x @ narrow.T, z @ wide.T, y @ short.T]  # distinct inputs: no sibling merge
+    planned, got = model_run(outputs)
+    gemvs = {s.attrs["segments"][0]["w"].shape: s for s in planned.steps if s.kind == K_GEMV}
+    assert gemvs[(384, 8192)].attrs["blocks"] == 4  # 24 tiles, 256 k-steps: 96 blocks of 64 k-steps
+    assert "blocks" not in gemvs[(8192, 2048)].attrs and "blocks" not in gemvs[(384, 256)].attrs
+    workspace, ticket_bytes = gemvs[(384, 8192)].attrs["workspace"], gemvs[(384, 8192)].attrs["ticket_bytes"]
+    assert ticket_bytes == 256  # 24 tickets, 256-byte aligned
+    assert workspace.size * 4 >= ticket_bytes + _planner.gemv_partial_bytes(gemvs[(384, 8192)], 4) == 256 + 24 * 4 * 1024
+    expected = realize(*outputs, compiler="cpu")
+    for value, reference in zip(got, expected):
+        np.testing.assert_allclose(np.asarray(value, np.float32), np.asarray(reference, np.float32), rtol=2e-2, atol=2e-2)

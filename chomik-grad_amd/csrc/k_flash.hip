@@ -5,8 +5,8 @@
 // float32, rounded once to the output dtype.  Scores are scaled into the
 // base-2 domain (s * log2(e) / d) so every exponential is one exp2.
 //
-// Block = 256 threads = 4 wavefronts, 64 query rows (16 per wave), key tiles
-// of 64.  Scores are computed transposed, S^T = K Q^T with
+// Block = 512 threads = 8 wavefronts, 128 query rows (16 per wave), key
+// tiles of 64: one K/V tile in LDS serves eight waves' MFMA work.  Scores are computed transposed, S^T = K Q^T with
 // v_mfma_f32_16x16x32 (A = 16 key rows, B = 16 query rows, k = head dims), so
 // lane (i, g) = (l % 16, l / 16) holds the scores of query i for keys
 // 16 t + 4 g + r, r = 0..3.  That is also the A-operand layout P V needs
@@ -16,8 +16,10 @@
 // comes from the lane that owns its scores (one shuffle per row).  V goes
 // through LDS transposed ([dim][key]) to supply the B operand; lanes write
 // consecutive keys of one dimension so the 16-bit transposing stores do not
-// collide.  The next tile's K and V are loaded into registers while the
-// current tile is computed.
+// collide.  K and V tiles are loaded two ahead into two register sets used
+// in turn (the loop handles two tiles per iteration, so every wait covers
+// exactly the set about to be stored); loads past the last tile re-read it
+// and keys past the cache are clamped and zeroed, so no load is conditional.
 //
 // When the planner has proved the mask is the causal triangle (0 on and below
 // the diagonal, one value v <= -1e4 above), key tiles above the diagonal are
@@ -34,7 +36,8 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef __bf16 b8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-constexpr int kD = 64, kBQ = 64, kBK = 64;
+constexpr int kD = 64, kWaves = 8, kBQ = 16 * kWaves, kBK = 64;
+constexpr int kFlashThreads = 64 * kWaves;
 constexpr int kKRow = kD + 8;   // LDS row of the K tile (elements)
 constexpr int kVRow = kBK + 8;  // LDS row of the transposed V tile (elements)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -61,7 +64,7 @@ template <> struct FlashMfma<bf16_t> {
 // 16-byte boundaries, n[26..28] out strides (b, h, t; unit along hd);
 // f[0] d, f[1] the causal mask's value above the diagonal.
 template <typename T>
-__global__ __launch_bounds__(256) void k_flash_prefill(KArgs a) {
+__global__ __launch_bounds__(kFlashThreads) void k_flash_prefill(KArgs a) {
   using E = Elem<T>;
   using F = FlashMfma<T>;
   __shared__ __attribute__((aligned(16))) T Ks[kBK * kKRow];
@@ -96,32 +99,28 @@ __global__ __launch_bounds__(256) void k_flash_prefill(KArgs a) {
   const float scale = kLog2e / E::round(a.f[0]);  // scores in units of log2
   const uint4 zero = make_uint4(0, 0, 0, 0);
 
-  // Tile loads: K rows 16 bytes per thread (key tid / 8, dims 8 (tid % 8));
-  // V with consecutive keys across lanes (key tid % 64, dims 8 c) so the
-  // transposing 16-bit stores of one dimension land in consecutive words.
-  uint4 kreg[2], vreg[2];
-  auto load_tile = [&](int64_t j0) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int v = tid + 256 * t, r = v >> 3, c = v & 7;
-      const int64_t key = j0 + r;
-      kreg[t] = key < C ? *reinterpret_cast<const uint4*>(Kp + key * kstride + 8 * c) : zero;
-      const int vr = tid & 63, vc = (tid >> 6) + 4 * t;
-      const int64_t vkey = j0 + vr;
-      vreg[t] = vkey < C ? *reinterpret_cast<const uint4*>(Vp + vkey * vstride + 8 * vc) : zero;
-    }
+  // Tile loads, one K and one V vector per thread: K rows 16 bytes per
+  // thread (key tid / 8, dims 8 (tid % 8)); V with consecutive keys across
+  // lanes (key tid % 64, dims 8 (tid / 64)) so the transposing 16-bit stores
+  // of one dimension land in consecutive words.
+  static_assert(kBK * kD / 8 == kFlashThreads, "one K and one V vector per thread");
+  struct TileRegs {
+    uint4 k, v;
   };
-  auto store_tile = [&]() {
+  auto load_tile = [&](TileRegs& t, int64_t j0) {
+    const int64_t key = j0 + (tid >> 3), vkey = j0 + (tid & 63);
+    const uint4 k = *reinterpret_cast<const uint4*>(Kp + (key < C ? key : C - 1) * kstride + 8 * (tid & 7));
+    const uint4 v = *reinterpret_cast<const uint4*>(Vp + (vkey < C ? vkey : C - 1) * vstride + 8 * (tid >> 6));
+    t.k = key < C ? k : zero;
+    t.v = vkey < C ? v : zero;
+  };
+  auto store_tile = [&](const TileRegs& t) {
+    *reinterpret_cast<uint4*>(&Ks[(tid >> 3) * kKRow + 8 * (tid & 7)]) = t.k;
+    const int vr = tid & 63, vc = tid >> 6;
+    const uint32_t words[4] = {t.v.x, t.v.y, t.v.z, t.v.w};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int v = tid + 256 * t, r = v >> 3, c = v & 7;
-      *reinterpret_cast<uint4*>(&Ks[r * kKRow + 8 * c]) = kreg[t];
-      const int vr = tid & 63, vc = (tid >> 6) + 4 * t;
-      const uint32_t words[4] = {vreg[t].x, vreg[t].y, vreg[t].z, vreg[t].w};
-#pragma unroll
-      for (int d = 0; d < 8; ++d)
-        Vt[(8 * vc + d) * kVRow + vr] = static_cast<uint16_t>((d & 1) ? (words[d >> 1] >> 16) : (words[d >> 1] & 0xffffu));
-    }
+    for (int d = 0; d < 8; ++d)
+      Vt[(8 * vc + d) * kVRow + vr] = static_cast<uint16_t>((d & 1) ? (words[d >> 1] >> 16) : (words[d >> 1] & 0xffffu));
   };
 
   float m = -INFINITY, lsum = 0.f;  // running max (log2 units) and partial sum of this lane's keys
@@ -129,14 +128,7 @@ __global__ __launch_bounds__(256) void k_flash_prefill(KArgs a) {
 #pragma unroll
   for (int tn = 0; tn < 4; ++tn) o[tn] = f4v{0.f, 0.f, 0.f, 0.f};
 
-  load_tile(0);
-#pragma unroll 1
-  for (int64_t j0 = 0; j0 < kend; j0 += kBK) {
-    __syncthreads();  // the previous tile's LDS reads are done
-    store_tile();
-    __syncthreads();
-    if (j0 + kBK < kend) load_tile(j0 + kBK);  // in flight during this tile's math
-
+  auto compute = [&](int64_t j0) {
     f4v st[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -204,6 +196,27 @@ __global__ __launch_bounds__(256) void k_flash_prefill(KArgs a) {
         o[tn] = F::step(pa, make_uint4(lo.x, lo.y, hi.x, hi.y), o[tn]);
       }
     }
+  };
+
+  // two tiles per iteration, register sets ta and tb in turn; a load past
+  // the last tile re-reads the last one (a cache hit, never used)
+  const int64_t last = ((kend - 1) / kBK) * kBK;
+  TileRegs ta, tb;
+  load_tile(ta, 0);
+  load_tile(tb, kBK < kend ? kBK : last);
+#pragma unroll 1
+  for (int64_t j0 = 0; j0 < kend; j0 += 2 * kBK) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    store_tile(ta);
+    __syncthreads();
+    load_tile(ta, j0 + 2 * kBK < kend ? j0 + 2 * kBK : last);  // in flight during two tiles' math
+    compute(j0);
+    if (j0 + kBK >= kend) break;
+    __syncthreads();
+    store_tile(tb);
+    __syncthreads();
+    load_tile(tb, j0 + 3 * kBK < kend ? j0 + 3 * kBK : last);
+    compute(j0 + kBK);
   }
   // row sums: this lane's keys, then the other three key groups of its query
   lsum += __shfl_xor(lsum, 16, 64);
@@ -241,7 +254,7 @@ bool plan_flash_prefill(KArgs& a, Launch& l) {
   l.func = dt == F16 ? reinterpret_cast<const void*>(&k_flash_prefill<__half>)
                      : reinterpret_cast<const void*>(&k_flash_prefill<bf16_t>);
   l.grid = dim3(static_cast<unsigned>(blocks));
-  l.block = dim3(256);
+  l.block = dim3(kFlashThreads);
   l.shmem = 0;
   return true;
 }

@@ -63,8 +63,10 @@ template <> struct FlashMfma<bf16_t> {
 // n[23] mask dtype, n[24] causal mask proved, n[25] q, K, V views start on
 // 16-byte boundaries, n[26..28] out strides (b, h, t; unit along hd);
 // f[0] d, f[1] the causal mask's value above the diagonal.
+// At most 128 VGPRs (four waves per SIMD): two 8-wave blocks per CU.
 template <typename T>
-__global__ __launch_bounds__(kFlashThreads) void k_flash_prefill(KArgs a) {
+__global__ __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void k_flash_prefill(KArgs a) {
   using E = Elem<T>;
   using F = FlashMfma<T>;
   __shared__ __attribute__((aligned(16))) T Ks[kBK * kKRow];
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(kFlashThreads) void k_flash_prefill(KArgs a) {
   const T* Mp = static_cast<const T*>(a.p[3]);
   const int64_t mrow = b * a.n[19] + h * a.n[20] + (my_q < Tq ? my_q : Tq - 1) * a.n[21];
   const int64_t kend = causal ? (C < q0 + kBQ ? C : q0 + kBQ) : C;
-  const float scale = kLog2e / E::round(a.f[0]);  // scores in units of log2
+  const float scale = kLog2e / E::round(a.f[0]);  // raw score -> units of log2
   const uint4 zero = make_uint4(0, 0, 0, 0);
 
   // Tile loads, one K and one V vector per thread: K rows 16 bytes per
@@ -123,7 +125,7 @@ __global__ __launch_bounds__(kFlashThreads) void k_flash_prefill(KArgs a) {
       Vt[(8 * vc + d) * kVRow + vr] = static_cast<uint16_t>((d & 1) ? (words[d >> 1] >> 16) : (words[d >> 1] & 0xffffu));
   };
 
-  float m = -INFINITY, lsum = 0.f;  // running max (log2 units) and partial sum of this lane's keys
+  float m = -INFINITY, lsum = 0.f;  // running raw-score max and partial exp-sum of this lane's keys
   f4v o[4];
 #pragma unroll
   for (int tn = 0; tn < 4; ++tn) o[tn] = f4v{0.f, 0.f, 0.f, 0.f};
@@ -139,45 +141,63 @@ __global__ __launch_bounds__(kFlashThreads) void k_flash_prefill(KArgs a) {
         st[t] = F::step(ka, qf[ks], st[t]);
       }
     }
-    // scaled scores of query my_q at keys j0 + 16 t + 4 fg + r; the tile maximum
-    const bool diagonal = causal && j0 + kBK > q0;
+    // Scores of query my_q at keys j0 + 16 t + 4 fg + r, kept raw: the
+    // running maximum m is in raw units and the scale folds into one fma per
+    // exponent.  Only edge tiles (the causal diagonal, keys past the cache,
+    // an explicit mask) mask per key; tiles below every query of the block
+    // take the plain path.
+    const bool edge = has_mask || j0 + kBK > C || (causal && j0 + kBK > q0);
     float x[4][4];
     float tmax = -INFINITY;
+    if (edge) {
+      const int key0 = static_cast<int>(j0) + 4 * fg, c32 = static_cast<int>(C), q32 = static_cast<int>(my_q);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t key = j0 + 16 * t + 4 * fg + r;
-        float s = st[t][r];
-        if (has_mask && key < C) s += E::to_f(Mp[mrow + key * a.n[22]]) * E::round(a.f[0]);
-        s *= scale;
-        const bool dead = key >= C || (diagonal && key > my_q);
-        x[t][r] = dead ? -INFINITY : s;
-        tmax = fmaxf(tmax, x[t][r]);
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int key = key0 + 16 * t + r;
+          float sv = st[t][r];
+          if (has_mask && key < c32) sv += E::to_f(Mp[mrow + key * a.n[22]]) * E::round(a.f[0]);
+          const bool dead = key >= c32 || (causal && key > q32);
+          x[t][r] = dead ? -INFINITY : sv;
+          tmax = fmaxf(tmax, x[t][r]);
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[t][r] = st[t][r];
+          tmax = fmaxf(tmax, x[t][r]);
+        }
+    }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float mnew = fmaxf(m, tmax);
     // every query has an unmasked key in its first tile, so mnew is finite
     // from the first tile on (a -inf - -inf would need an all-masked row)
-    const float alpha = exp2f(m - mnew);
+    const float alpha = exp2f((m - mnew) * scale);
     m = mnew;
+    const float mscaled = mnew * scale;
     float p[4][4];
     float psum = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[t][r] = exp2f(x[t][r] - mnew);
+        p[t][r] = exp2f(fmaf(x[t][r], scale, -mscaled));
         psum += p[t][r];
       }
     lsum = lsum * alpha + psum;
-    // rescale O rows (queries 4 fg + r) by their own alpha
+    // rescale O rows (queries 4 fg + r) by their own alpha, unless no row
+    // of the wave raised its maximum (alpha == 1 everywhere)
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(alpha, 4 * fg + r, 64);
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * fg + r, 64);
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) o[tn][r] *= ar;
+        for (int tn = 0; tn < 4; ++tn) o[tn][r] *= ar;
+      }
     }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {

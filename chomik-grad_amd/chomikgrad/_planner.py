@@ -588,7 +588,41 @@ class Emitter:
             view = PV(a.shape, node.dtype, strides, dense.storage, dense.offset)
             self.add(K_COPY, [a], [view])
             return out
+        row = self._one_hot_row(a, b, node)
+        if row is not None:
+            # e_s^T @ B: row s of B (the prefill's last-position selector,
+            # llama.py LlamaForCausalLM._forward): a copy of that row
+            view = PV(tuple(node.shape), node.dtype, b.strides, b.storage, b.offset + row * b.strides[-2])
+            out = self.new_value(node.shape, node.dtype, "selected_row")
+            self.add(K_COPY, [view], [out])
+            return out
         return self.matmul(node, a, b)
+
+    @staticmethod
+    def _one_hot_row(a: PV, b: PV, node) -> Optional[int]:
+        """a is a captured constant (1, S) row holding a single 1 and zeros, b
+        is (..., S, D) of the same dtype: then a @ b is row s of b.  (As for
+        the placement, only for finite B does this equal the float product.)"""
+        if len(a.shape) != 2 or a.shape[0] != 1 or a.storage.kind != "const" or len(b.shape) < 2:
+            return None
+        if not (a.dtype == b.dtype == node.dtype) or a.shape[1] != b.shape[-2]:
+            return None
+        if tuple(node.shape) != tuple(b.shape[:-2]) + (1, b.shape[-1]):
+            return None
+        leaf = getattr(a.storage, "leaf", None)
+        if leaf is None or leaf.value is None:
+            return None
+        value = np.asarray(leaf.value)
+        if value.dtype == BFLOAT16:
+            from .dtypes import bf16_to_float32
+            value = bf16_to_float32(value)
+        value = value.astype(np.float32).reshape(-1)
+        if value.size != a.shape[1]:
+            return None
+        hot = np.flatnonzero(value)
+        if hot.size != 1 or value[hot[0]] != 1.0:
+            return None
+        return int(hot[0])
 
     @staticmethod
     def _is_placement(a: PV, b: PV, node) -> bool:

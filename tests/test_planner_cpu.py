@@ -182,9 +182,9 @@ def test_half_precision_prefill_uses_mfma_gemm(dtype):
     assert sum(g.attrs.get("res") is not None for g in gemms) == 2
     assert not any(s.kind == K_ELEMENTWISE for s in planned.steps)
     # the cache placements K^T @ eye(S, C) become fill + strided copy; the one
-    # generic matmul left is the last-row selector
+    # the last-row selector (a one-hot constant) is a row copy: no generic matmul left
     assert sum(s.kind == K_FILL for s in planned.steps) == 2
-    assert sum(s.kind == K_MATMUL for s in planned.steps) == 1
+    assert sum(s.kind == K_MATMUL for s in planned.steps) == 0
     for value, reference in zip(got, expected):
         v, r = np.asarray(value), np.asarray(reference)
         if dtype is BFLOAT16:

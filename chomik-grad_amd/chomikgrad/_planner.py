@@ -58,10 +58,12 @@ GEMV_STAGE_BYTES = 48 * 1024
 # Waves sharing one GEMV row group (K split): 0 lets the kernel choose from
 # the row count; CHOMIK_HIP_GEMV_SPLIT=1/2/4 forces one (for tuning sweeps).
 GEMV_SPLIT = int(os.environ.get("CHOMIK_HIP_GEMV_SPLIT", "0"))
-# Decode attention: cache rows per workgroup = (32 for 2-byte, 16 for 4-byte
-# dtypes) x passes; 0 picks the passes from the shape, 1/2/4 forces them.
-# Decode attention: 0 chooses; 1, 2 or 4 force the chunk kernel with that
-# many passes per workgroup; -1 forces the streaming kernel.
+# Decode attention (cache rows per pass: 32 for 2-byte, 16 for 4-byte
+# dtypes): 0 chooses; 1, 2 or 4 force the chunk kernel with that
+# many passes per workgroup; -1 forces the streaming kernel; -2 the MFMA
+# kernel where it applies (16-bit caches of at most 768 rows; one workgroup
+# per KV head, measured slower than the chunk kernel at the C2 shape: one CU
+# keeps too few HBM misses in flight for 160 KB, so it is never chosen).
 DECODE_ATTN_PASSES = int(os.environ.get("CHOMIK_HIP_ATTN_PASSES", "0"))
 DECODE_ATTN_MAX_CHUNKS = 64
 # The streaming kernel takes over when the chunk kernel would need more than
@@ -71,6 +73,14 @@ DECODE_ATTN_MAX_CHUNKS = 64
 DECODE_ATTN_STREAM_ABOVE = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_ABOVE", "768"))
 DECODE_ATTN_STREAM_WGS = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_WGS", "768"))
 DECODE_ATTN_STREAM_UNROLL = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_UNROLL", "2"))
+# tiles one streaming workgroup may cover (it flags tiles with blended rows
+# in a 64-bit mask)
+DECODE_ATTN_STREAM_MAX_TILES = 64
+# The MFMA kernel: one workgroup of at most 8 waves per (sequence, KV head),
+# each wave with 1-3 blocks of 32 cache rows in registers.
+DECODE_ATTN_MFMA_BLOCK = 32
+DECODE_ATTN_MFMA_WAVES = 8
+DECODE_ATTN_MFMA_MAX_BLOCKS = 3
 SDPA_MAX_KEYS = 32768
 ARENA_ALIGN = 256
 SUPPORTED_TAGS = frozenset({"rms_norm", "rope", "sdpa", "softmax"})
@@ -1126,14 +1136,21 @@ def decode_attention_passes(B: int, KV: int, C: int, itemsize: int) -> int:
 
 
 def decode_attention_plan(B: int, KV: int, C: int, G: int, itemsize: int, divisor: float = 8.0) -> Dict[str, int]:
-    """Kernel choice for the fused decode attention: ``passes`` > 0 is the
-    chunk kernel (``chunks`` workgroups per KV head); ``passes`` 0 is the
+    """Kernel choice for the fused decode attention: ``passes`` 1, 2 or 4 is
+    the chunk kernel (``chunks`` workgroups per KV head); ``passes`` 0 is the
     streaming kernel, whose ``chunks`` workgroups per KV head each stream
-    ``rows`` cache rows in tiles of ``unroll`` passes."""
+    ``rows`` cache rows in tiles of ``unroll`` passes; ``passes`` 8 is the
+    MFMA kernel, one workgroup per KV head whose waves hold ``rows`` blocks
+    of 32 cache rows each.  ``rows`` is the kernel's n[29] in both cases."""
     rpp = decode_attention_rows(itemsize)
     pow2 = divisor > 0 and math.frexp(divisor)[0] == 0.5
+    blocks = -(-C // DECODE_ATTN_MFMA_BLOCK)
+    if (itemsize == 2 and pow2 and DECODE_ATTN_PASSES == -2
+            and blocks <= DECODE_ATTN_MFMA_WAVES * DECODE_ATTN_MFMA_MAX_BLOCKS):
+        per_wave = -(-blocks // DECODE_ATTN_MFMA_WAVES)
+        return {"passes": 8, "chunks": 1, "rows": per_wave, "unroll": 0}
     stream = DECODE_ATTN_PASSES == -1
-    if DECODE_ATTN_PASSES == 0:
+    if DECODE_ATTN_PASSES in (0, -2):  # -2 where the MFMA kernel does not apply: as 0
         biggest = -(-C // (rpp * 4))
         stream = B * KV * biggest > DECODE_ATTN_STREAM_ABOVE or biggest > DECODE_ATTN_MAX_CHUNKS
     # the streaming kernel multiplies by the reciprocal of the score divisor,
@@ -1142,10 +1159,12 @@ def decode_attention_plan(B: int, KV: int, C: int, G: int, itemsize: int, diviso
     if not stream:
         passes = decode_attention_passes(B, KV, C, itemsize)
         return {"passes": passes, "chunks": -(-C // (rpp * passes)), "rows": 0, "unroll": 0}
+    unroll = DECODE_ATTN_STREAM_UNROLL
     target = max(1, min(DECODE_ATTN_MAX_CHUNKS, -(-DECODE_ATTN_STREAM_WGS // (B * KV))))
+    # a workgroup streams at most DECODE_ATTN_STREAM_MAX_TILES tiles
+    target = min(DECODE_ATTN_MAX_CHUNKS, max(target, -(-C // (DECODE_ATTN_STREAM_MAX_TILES * rpp * unroll))))
     rows = -(-C // target)
     rows = -(-rows // rpp) * rpp
-    unroll = DECODE_ATTN_STREAM_UNROLL
     return {"passes": 0, "chunks": -(-C // rows), "rows": rows, "unroll": unroll}
 
 

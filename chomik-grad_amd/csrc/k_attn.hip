@@ -501,21 +501,21 @@ __device__ __forceinline__ uint4 buffer_row(__amdgpu_buffer_rsrc_t r, int off) {
 // short caches its one latency chain is the kernel's time, but a long cache
 // becomes thousands of workgroups that run in several latency-bound rounds.
 // Here a workgroup owns a range of L rows (n[29], a multiple of the rows per
-// pass; NS = ceil(C / L) ranges per (sequence, KV head)) and streams it in
-// tiles of U passes.  K and V are staggered so that one register set of each
-// suffices: the next tile's K rows (with its write-mask and mask values) are
-// loaded as soon as the current tile is scored, and its V rows as soon as the
-// current tile is accumulated, so each load has the other half's work to
-// arrive.  Loads are buffer loads at loop-invariant 32-bit offsets plus the
-// tile's offset; rows past the cache read 0, and the prefetch after the last
-// tile uses an out-of-range offset (zeros, no memory traffic), so the loop
-// has no peeled tail.  Each row group (the LPR lanes
-// sharing a row) keeps an online softmax per query head -- running maximum
-// and exp-sum, rescaled once per tile -- and its lanes' slices of P V in
-// registers, so V is never staged in LDS.  A tile without blended rows (the
-// common case in place: only the new token's row has w != 0) takes a path
-// without the blend and the cache stores, chosen once per wave.  At the end
-// the row groups of a wave merge by shuffles and the waves through LDS; the
+// pass, at most 64 tiles; NS = ceil(C / L) ranges per (sequence, KV head))
+// and streams it in tiles of U passes.  Two register sets alternate, so two
+// tiles of K and V (with their write-mask and mask values) are in flight
+// while one is scored and accumulated: tile t + 2 is loaded into the set
+// that tile t has just left.  Loads are buffer loads at loop-invariant 32-bit
+// offsets plus the tile's offset; rows past the cache read 0, and the loads
+// past the last tile use an out-of-range offset (zeros, no memory traffic),
+// so the loop has no peeled tail.  Each row group (the LPR lanes sharing a
+// row) keeps an online softmax per query head -- running maximum and
+// exp-sum, rescaled once per tile -- and its lanes' slices of P V in
+// registers, so V is never staged in LDS.  The main pass leaves out the rows
+// with w != 0 (in place: only the new token's row); a tile holding any is
+// flagged, the first one per wave kept in LDS, and after the loop those rows
+// are blended, written to the cache, scored and accumulated.  At the end the
+// row groups of a wave merge by shuffles and the waves through LDS; the
 // workgroup writes the chunk kernel's partials (or the output, when one
 // range covers the cache) and the same combine follows.  Scores, blended
 // rows and cache writes keep the chunk kernel's rounding; the score divisor
@@ -536,6 +536,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
   __shared__ float ks[kHead], vs[kHead];
   __shared__ float wmax[NW][G], wsum[NW][G];
   __shared__ float wacc[NW][G][kHead];
+  __shared__ uint4 stash_k[U][kThreads], stash_v[U][kThreads];
+  __shared__ float stash_w[U][kThreads], stash_m[U][kThreads];
 
   const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
   const int64_t L = a.n[29];
@@ -573,31 +575,39 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
     moff[u] = static_cast<int>((head * mh + r * mc) * S);
   }
 
-  uint4 kbuf[U], vbuf[U];
-  float wbuf[U], mbuf[U];
+  // One tile's rows in registers: K, V, write-mask and mask values.
+  struct Tile {
+    uint4 k[U], v[U];
+    float w[U], m[U];
+  };
   // Tile t's loads; past the last tile every offset is out of range, so
   // the loads return 0 without touching memory.
   constexpr int kPast = 0x7fff0000;
-  auto issue_k = [&](int64_t t) {
+  auto issue_k = [&](Tile& x, int64_t t) {
     const int64_t r0 = c0 + t * TR;
     const bool in = t < ntiles;
     const int tk = in ? static_cast<int>(r0 * kHead * S) : kPast, tw = in ? static_cast<int>(r0 * wc * S) : kPast,
               tm = in ? static_cast<int>(r0 * mc * S) : kPast;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      kbuf[u] = buffer_row(krs, koff[u] + tk);
-      wbuf[u] = buffer_scalar<T>(wrs, woff[u] + tw);
+      x.k[u] = buffer_row(krs, koff[u] + tk);
+      x.w[u] = buffer_scalar<T>(wrs, woff[u] + tw);
       const float mv = buffer_scalar<T>(mrs, moff[u] + tm);
-      mbuf[u] = masked ? mv : 0.f;
+      x.m[u] = masked ? mv : 0.f;
     }
   };
-  auto issue_v = [&](int64_t t) {
+  auto issue_v = [&](Tile& x, int64_t t) {
     const int tk = t < ntiles ? static_cast<int>((c0 + t * TR) * kHead * S) : kPast;
 #pragma unroll
-    for (int u = 0; u < U; ++u) vbuf[u] = buffer_row(vrs, koff[u] + tk);
+    for (int u = 0; u < U; ++u) x.v[u] = buffer_row(vrs, koff[u] + tk);
   };
-  issue_k(0);
-  issue_v(0);
+  // Two tiles in flight per wave: tile t + 2 is loaded into the register set
+  // that tile t just left.
+  Tile ta, tb;
+  issue_k(ta, 0);
+  issue_v(ta, 0);
+  issue_k(tb, 1);
+  issue_v(tb, 1);
 
   // -- RoPE of q and k (the position load, then the table).
   const int32_t* positions = static_cast<const int32_t*>(a.p[3]);
@@ -652,13 +662,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
 #pragma unroll
     for (int e = 0; e < V; ++e) acc[h][e] = 0.f;
   }
-  // the new token's k' and v slices of this lane, packed in T (exact)
-  const uint4 knew = pack<T>(&ks[part * V]), vnew = pack<T>(&vs[part * V]);
-  // Blend of a cache row with the new row.  The fresh values pass through an
-  // empty asm first, so nothing derived from them is hoisted out of the rare
-  // slow path into registers held across the whole loop.
+  // Blend of a cache row with the new row.
   auto blend = [&](uint4& row, float w, uint4 fresh) {
-    asm volatile("" : "+v"(fresh.x), "+v"(fresh.y), "+v"(fresh.z), "+v"(fresh.w));
     float x[V], f[V];
     unpack<T>(row, x);
     unpack<T>(fresh, f);
@@ -672,43 +677,22 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
   // the cache row of row j: in place, or the new buffer's contiguous layout
   auto dst_row = [&](int64_t j) { return in_place ? cb + j * kHead : ((b * KV + g) * C + j) * kHead; };
 
-  float s[U][G], wt[U];
-  // Slow path of a tile (chosen once per wave): the rows with w != 0 are
-  // blended in their register buffers and written to the cache (every row
-  // is written when the cache goes to a new buffer); the shared scoring and
-  // accumulation below then see the blended rows.
-  auto prep_k = [&](int64_t t) {
+  float s[U][G];
+  // Scores of the tile's U rows for all G heads from the rows as given (the
+  // reduce-scatter leaves each lane one head's dot product; the row group
+  // then shares them) and one rescale of the running state.  The main pass
+  // scores the rows with w == 0 (blended = false), the patch those with
+  // w != 0; the other rows, and rows outside the range, score -inf.
+  auto score = [&](const uint4 (&rows)[U], const Tile& x, int64_t t, bool blended) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = c0 + t * TR + u * RPP + rgi;
-      const float w = wbuf[u];
-      if (w != 0.f) blend(kbuf[u], w, knew);
-      if (j < c1 && (!in_place || w != 0.f)) reinterpret_cast<uint4*>(Ko + dst_row(j))[part] = kbuf[u];
-    }
-  };
-  auto prep_v = [&](int64_t t) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = c0 + t * TR + u * RPP + rgi;
-      const float w = wt[u];
-      if (w != 0.f) blend(vbuf[u], w, vnew);
-      if (j < c1 && (!in_place || w != 0.f)) reinterpret_cast<uint4*>(Vo + dst_row(j))[part] = vbuf[u];
-    }
-  };
-  // Scores of the tile's U rows for all G heads (the reduce-scatter leaves
-  // each lane one head's dot product; the row group then shares them) and
-  // one rescale of the running state.
-  auto score = [&](int64_t t) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = c0 + t * TR + u * RPP + rgi;
-      wt[u] = wbuf[u];
       float d[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) d[h] = RowDot<T>::dot(kbuf[u], qp[h]);
+      for (int h = 0; h < G; ++h) d[h] = RowDot<T>::dot(rows[u], qp[h]);
       float sc = E::round(E::round(reduce_scatter<G, LPR>(d, part)) * rdiv);
-      sc = E::round(sc + mbuf[u]);
-      sc = j < c1 ? sc : -INFINITY;
+      sc = E::round(sc + x.m[u]);
+      sc = (j < c1 && (x.w[u] != 0.f) == blended) ? sc : -INFINITY;
 #pragma unroll
       for (int h = 0; h < G; ++h) s[u][h] = G == 1 ? sc : __shfl(sc, (lane & ~(LPR - 1)) + h * (LPR / G), 64);
     }
@@ -724,13 +708,12 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
       for (int e = 0; e < V; ++e) acc[h][e] *= f;
     }
   };
-  // exp-sums and P V of the tile's rows.
-  auto accumulate = [&](int64_t t) {
+  // exp-sums and P V of the tile's rows (a row scored -inf adds nothing).
+  auto accumulate = [&](const uint4 (&rows)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = c0 + t * TR + u * RPP + rgi;
       float vf[V];
-      unpack<T>(j < c1 ? vbuf[u] : make_uint4(0, 0, 0, 0), vf);
+      unpack<T>(rows[u], vf);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const float p = s[u][h] == -INFINITY ? 0.f : __expf(s[u][h] - m[h]);
@@ -740,22 +723,95 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
       }
     }
   };
-  // blended rows or a copied cache make the tile slow, for the whole wave
-  auto slow_tile = [&]() {
-    bool any = !in_place;
+  // A copied cache takes every row of the range that is not blended, as read.
+  auto copy_rows = [&](const uint4 (&rows)[U], const Tile& x, int64_t t, T* dst) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) any = any || wbuf[u] != 0.f;
-    return __any(any) != 0;
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      if (j < c1 && x.w[u] == 0.f) reinterpret_cast<uint4*>(dst + dst_row(j))[part] = rows[u];
+    }
+  };
+  // Rows with w != 0 (in place: only the new token's row, in one tile of the
+  // cache) are left out of the main pass and handled here, for the whole
+  // wave: blended into temporaries, written to the cache, then scored and
+  // accumulated like the others.  Blending in the tile's own registers would
+  // make the compiler keep a second copy of both register sets.
+  auto patch = [&](const Tile& x, int64_t t) {
+    // the new token's k' and v slices of this lane, packed in T (exact)
+    const uint4 knew = pack<T>(&ks[part * V]), vnew = pack<T>(&vs[part * V]);
+    uint4 kb[U], vb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      const float w = x.w[u];
+      kb[u] = x.k[u];
+      vb[u] = x.v[u];
+      if (w != 0.f) {
+        blend(kb[u], w, knew);
+        blend(vb[u], w, vnew);
+        if (j < c1) {
+          reinterpret_cast<uint4*>(Ko + dst_row(j))[part] = kb[u];
+          reinterpret_cast<uint4*>(Vo + dst_row(j))[part] = vb[u];
+        }
+      }
+    }
+    score(kb, x, t, true);
+    accumulate(vb);
+  };
+  // Tile t from register set x, whose next tile is t + 2.  A tile past the
+  // range (the second of the last pair when the count is odd) reads zeros
+  // and scores -inf: it changes nothing.  A tile with rows to blend is only
+  // flagged here (bit t of pending), and the first such tile of the wave is
+  // kept in LDS; patch() runs after the loop, so that no register of the
+  // loop is modified under a branch (which would make the compiler hold a
+  // second copy of both register sets).
+  uint64_t pending = 0;  // wave-uniform
+  int64_t stashed = -1;
+  auto step = [&](Tile& x, int64_t t) {
+    score(x.k, x, t, false);
+    if (!in_place) copy_rows(x.k, x, t, Ko);
+    accumulate(x.v);
+    if (!in_place) copy_rows(x.v, x, t, Vo);
+    bool any = false;
+#pragma unroll
+    for (int u = 0; u < U; ++u) any = any || x.w[u] != 0.f;
+    if (__any(any)) {
+      pending |= uint64_t(1) << t;
+      if (stashed < 0) {
+        stashed = t;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          stash_k[u][tid] = x.k[u];
+          stash_v[u][tid] = x.v[u];
+          stash_w[u][tid] = x.w[u];
+          stash_m[u][tid] = x.m[u];
+        }
+      }
+    }
+    issue_k(x, t + 2);
+    issue_v(x, t + 2);
   };
 
-  for (int64_t t = 0; t < ntiles; ++t) {
-    const bool slow = slow_tile();
-    if (slow) prep_k(t);
-    score(t);
-    issue_k(t + 1);
-    if (slow) prep_v(t);
-    accumulate(t);
-    issue_v(t + 1);
+  for (int64_t t = 0; t < ntiles; t += 2) {
+    step(ta, t);
+    step(tb, t + 1);
+  }
+  while (pending) {
+    const int64_t t = __builtin_ctzll(pending);
+    pending &= pending - 1;
+    if (t == stashed) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ta.k[u] = stash_k[u][tid];
+        ta.v[u] = stash_v[u][tid];
+        ta.w[u] = stash_w[u][tid];
+        ta.m[u] = stash_m[u][tid];
+      }
+    } else {
+      issue_k(ta, t);
+      issue_v(ta, t);
+    }
+    patch(ta, t);
   }
 
   // -- merge the row groups of each wave (shuffles), then the waves (LDS).
@@ -819,6 +875,303 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
   combine_chunks<T, G>(a, b, g, NS);
 }
 
+// ------------------------------------------------------------ short caches on MFMA
+// One workgroup per (sequence, KV head) covers the whole cache (C <= 768
+// rows), so no partials and no combine: every load is issued at once -- a
+// single CU pulls the 160 KB of a 640-row head in about a microsecond when
+// nothing waits in between -- and the dot products run on the matrix cores.
+// Wave w owns NB blocks of 32 rows.  Scores: S (16 rows x 16 query-head
+// columns, heads >= G zero) = K (16 x 32 dims, v_mfma_f32_16x16x32, K rows
+// loaded straight into the A layout) x q^T, two per 16 rows.  P V: O (16
+// heads x 16 dims) += P (16 heads x 16 rows, the score tile's own layout,
+// rounded to the cache dtype) x V (16 rows x 16 dims, v_mfma_f32_16x16x16);
+// V rows are staged row-major in the wave's LDS tile and read as columns
+// (rows padded to 144 bytes: the four row groups of a column read hit
+// different banks).  RoPE is lane-local: a lane holds dims i and i + 32 of
+// its q (and k) slices.  The softmax is per wave (maximum and exp-sum over
+// its rows), then the waves merge through LDS.  Scores, blended rows and
+// cache writes keep the other kernels' rounding; the score divisor must be a
+// power of two, as for the streaming kernel.
+typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
+typedef short ms4 __attribute__((ext_vector_type(4)));
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef __bf16 mb8 __attribute__((ext_vector_type(8)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+template <typename T> struct AttnMfma;
+template <> struct AttnMfma<__half> {
+  __device__ static __forceinline__ mf4 qk(const uint4& k, const uint4& q, mf4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8, k), __builtin_bit_cast(mh8, q), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ mf4 pv(const uint2& p, const uint2& v, mf4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(mh4, p), __builtin_bit_cast(mh4, v), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t bits(float v) { return __half_as_ushort(__float2half(v)); }
+};
+template <> struct AttnMfma<bf16_t> {
+  __device__ static __forceinline__ mf4 qk(const uint4& k, const uint4& q, mf4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mb8, k), __builtin_bit_cast(mb8, q), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ mf4 pv(const uint2& p, const uint2& v, mf4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(ms4, p), __builtin_bit_cast(ms4, v), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t bits(float v) { return f32_to_bf16_bits(v); }
+};
+
+constexpr int kMfmaWaves = 8;   // waves per workgroup at most
+constexpr int kMfmaBlock = 32;  // cache rows per block
+constexpr int kVRow = 144;      // LDS bytes per staged V row
+
+// KArgs as k_decode_attn, with n[28] = 8 and n[29] = NB (blocks per wave);
+// the launch has ceil(ceil(C / 32) / NB) <= 8 waves.
+template <typename T, int G, int NB>
+__global__ __launch_bounds__(64 * kMfmaWaves) void k_decode_attn_mfma(KArgs a) {
+  using E = Elem<T>;
+  using M = AttnMfma<T>;
+  constexpr int S = 2;
+  __shared__ __align__(16) unsigned char vst[kMfmaWaves][kMfmaBlock * kVRow];
+  __shared__ float wmax[kMfmaWaves][16], wsum[kMfmaWaves][16];
+  __shared__ float wacc[kMfmaWaves][G][kHead];
+
+  const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
+  const int64_t b = blockIdx.x / KV, g = blockIdx.x % KV;
+  const int dt = E::code;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = blockDim.x >> 6;
+  const int col = lane & 15, grp = lane >> 4;  // MFMA column; k group of the lane
+  const int64_t cb = b * a.n[16] + g * a.n[17];
+  const int64_t wb = b * a.n[20], wc = a.n[21];
+  const bool masked = a.p[8] != nullptr;
+  const bool in_place = a.n[27] != 0;
+  const T* Wm = static_cast<const T*>(a.p[7]);
+  const T* Am = masked ? static_cast<const T*>(a.p[8]) + b * a.n[22] + g * G * a.n[23] : Wm + wb;
+  const int64_t mh = masked ? a.n[23] : 0, mc = masked ? a.n[24] : wc;
+  const auto krs = buffer_over(static_cast<const T*>(a.p[5]) + cb, C * kHead * S);
+  const auto vrs = buffer_over(static_cast<const T*>(a.p[6]) + cb, C * kHead * S);
+  const auto wrs = buffer_over(Wm + wb, ((C - 1) * wc + 1) * S);
+  const auto mrs = buffer_over(Am, ((G - 1) * mh + (C - 1) * mc + 1) * S);
+  const int hcol = col < G ? col : 0;
+  constexpr int kPast = 0x7fff0000;  // an offset past every resource: loads return 0
+
+  // -- issue every load of this wave's blocks: K in the A layout (row col,
+  // dims 32 d + 8 grp ...), V row-major (row lane / 8 + 8 q, dims 8 (lane % 8)
+  // ...), the write mask of those rows and the mask of the score tile's rows.
+  uint4 kr[NB][2][2], vr[NB][4];
+  float wk[NB][2], wv[NB][4], mk[NB][2][4];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int64_t r0 = static_cast<int64_t>(kMfmaBlock) * (wave * NB + i);
+    const bool live = r0 < C;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t row = r0 + 16 * h + col;
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+        kr[i][h][d] = buffer_row(krs, live ? static_cast<int>((row * kHead + 32 * d + 8 * grp) * S) : kPast);
+      wk[i][h] = buffer_scalar<T>(wrs, live ? static_cast<int>(row * wc * S) : kPast);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t srow = r0 + 16 * h + 4 * grp + r;
+        const float mv = buffer_scalar<T>(mrs, live ? static_cast<int>((hcol * mh + srow * mc) * S) : kPast);
+        mk[i][h][r] = masked ? mv : 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t row = r0 + (lane >> 3) + 8 * q;
+      vr[i][q] = buffer_row(vrs, live ? static_cast<int>((row * kHead + 8 * (lane & 7)) * S) : kPast);
+      wv[i][q] = buffer_scalar<T>(wrs, live ? static_cast<int>(row * wc * S) : kPast);
+    }
+  }
+
+  // -- q (B operand: head col, dims 32 d + 8 grp + e), the new k in the
+  // same dims and the new v in the V layout's dims; RoPE pairs dim i with
+  // dim i + 32, both held by the lane.
+  const int32_t* positions = static_cast<const int32_t*>(a.p[3]);
+  int64_t pos = a.n[14] == 2 ? positions[b] : positions[0];
+  float qx[2][8], kx[2][8], vx[8];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t dim = 32 * d + 8 * grp + e;
+      qx[d][e] = col < G ? load_f(a.p[0], b * a.n[5] + (g * G + col) * a.n[6] + dim * a.n[7], dt) : 0.f;
+      kx[d][e] = load_f(a.p[1], b * a.n[8] + g * a.n[9] + dim * a.n[10], dt);
+    }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vx[e] = load_f(a.p[2], b * a.n[11] + g * a.n[12] + (8 * (lane & 7) + e) * a.n[13], dt);
+  if (!(pos >= 0 && pos < a.n[15])) {
+    if (tid == 0) raise_error(a, ERR_POSITION);
+    pos = 0;
+  }
+  float cs[8], sn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    cs[e] = load_f(a.p[4], pos * kHead + 8 * grp + e, dt);
+    sn[e] = load_f(a.p[4], pos * kHead + 32 + 8 * grp + e, dt);
+  }
+  auto rope = [&](float (&x)[2][8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lo = x[0][e], hi = x[1][e];
+      x[0][e] = E::round(__fadd_rn(__fmul_rn(lo, cs[e]), __fmul_rn(hi, -sn[e])));
+      x[1][e] = E::round(__fadd_rn(__fmul_rn(lo, sn[e]), __fmul_rn(hi, cs[e])));
+    }
+  };
+  rope(qx);
+  rope(kx);
+  const uint4 qb[2] = {pack<T>(qx[0]), pack<T>(qx[1])};
+
+  // -- rows with w != 0 are blended with the new row; the cache rows of this
+  // workgroup are written (in place: the blended ones only).
+  auto blend = [&](uint4& row, float w, const float* fresh) {
+    float x[8];
+    unpack<T>(row, x);
+    const float keep = E::round(1.f - w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = E::round(E::round(x[e] * keep) + E::round(fresh[e] * w));
+    row = pack<T>(x);
+  };
+  T* Ko = static_cast<T*>(a.p[10]);
+  T* Vo = static_cast<T*>(a.p[11]);
+  auto dst_row = [&](int64_t j) { return in_place ? cb + j * kHead : ((b * KV + g) * C + j) * kHead; };
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int64_t r0 = static_cast<int64_t>(kMfmaBlock) * (wave * NB + i);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t row = r0 + 16 * h + col;
+      const float w = wk[i][h];
+      if (w != 0.f) {
+        blend(kr[i][h][0], w, kx[0]);
+        blend(kr[i][h][1], w, kx[1]);
+      }
+      if (row < C && (!in_place || w != 0.f)) {
+        reinterpret_cast<uint4*>(Ko + dst_row(row) + 8 * grp)[0] = kr[i][h][0];
+        reinterpret_cast<uint4*>(Ko + dst_row(row) + 32 + 8 * grp)[0] = kr[i][h][1];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t row = r0 + (lane >> 3) + 8 * q;
+      const float w = wv[i][q];
+      if (w != 0.f) blend(vr[i][q], w, vx);
+      if (row < C && (!in_place || w != 0.f)) reinterpret_cast<uint4*>(Vo + dst_row(row) + 8 * (lane & 7))[0] = vr[i][q];
+    }
+  }
+
+  // -- scores (lane: rows 16 h + 4 grp + r of each block, head col) and the
+  // wave's maximum per head
+  const float rdiv = 1.f / E::round(a.f[0]);  // exact: the divisor is a power of two
+  float sc[NB][2][4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int64_t r0 = static_cast<int64_t>(kMfmaBlock) * (wave * NB + i);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      mf4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = M::qk(kr[i][h][0], qb[0], acc);
+      acc = M::qk(kr[i][h][1], qb[1], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = r0 + 16 * h + 4 * grp + r;
+        float s = E::round(E::round(acc[r]) * rdiv);
+        s = E::round(s + mk[i][h][r]);
+        s = (row < C && col < G) ? s : -INFINITY;
+        sc[i][h][r] = s;
+        mx = nan_max(mx, s);
+      }
+    }
+  }
+  mx = nan_max(mx, __shfl_xor(mx, 16, 64));
+  mx = nan_max(mx, __shfl_xor(mx, 32, 64));
+
+  // -- P (rounded to the cache dtype; the exp-sum adds the rounded values)
+  // and P V through the wave's LDS tile
+  float ls = 0.f;
+  mf4 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = mf4{0.f, 0.f, 0.f, 0.f};
+  unsigned char* tile = vst[wave];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<uint4*>(tile + ((lane >> 3) + 8 * q) * kVRow + (lane & 7) * 16) = vr[i][q];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t pb[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float s = sc[i][h][r];
+        const float p = s == -INFINITY ? 0.f : __expf(s - mx);
+        pb[r] = M::bits(p);
+        ls += E::to_f(__builtin_bit_cast(T, static_cast<uint16_t>(pb[r])));
+      }
+      const uint2 pa = make_uint2(pb[0] | (pb[1] << 16), pb[2] | (pb[3] << 16));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        uint32_t vv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          vv[e] = *reinterpret_cast<const uint16_t*>(tile + (16 * h + 4 * grp + e) * kVRow + (16 * db + col) * 2);
+        o[db] = M::pv(pa, make_uint2(vv[0] | (vv[1] << 16), vv[2] | (vv[3] << 16)), o[db]);
+      }
+    }
+  }
+  ls += __shfl_xor(ls, 16, 64);
+  ls += __shfl_xor(ls, 32, 64);
+
+  // -- merge the waves: O (lane: heads 4 grp + r, dim 16 db + col), maxima
+  // and exp-sums per head
+  if (grp == 0) {
+    wmax[wave][col] = mx;
+    wsum[wave][col] = ls;
+  }
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int head = 4 * grp + r;
+      if (head < G) wacc[wave][head][16 * db + col] = o[db][r];
+    }
+  __syncthreads();
+  T* out = static_cast<T*>(a.p[9]);
+  for (int t = tid; t < G * kHead; t += blockDim.x) {
+    const int h = t / kHead, d = t % kHead;
+    float Mx = wmax[0][h];
+    for (int w = 1; w < nw; ++w) Mx = nan_max(Mx, wmax[w][h]);
+    float ov = 0.f, lv = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      const float f = wmax[w][h] == Mx ? 1.f : __expf(wmax[w][h] - Mx);
+      ov = fmaf(wacc[w][h][d], f, ov);
+      lv = fmaf(wsum[w][h], f, lv);
+    }
+    out[(b * H + g * G + h) * kHead + d] = E::from_f(ov / lv);
+  }
+}
+
+template <typename T, int G>
+const void* pick_mfma_nb(int nb) {
+  switch (nb) {
+    case 1: return reinterpret_cast<const void*>(&k_decode_attn_mfma<T, G, 1>);
+    case 2: return reinterpret_cast<const void*>(&k_decode_attn_mfma<T, G, 2>);
+    case 3: return reinterpret_cast<const void*>(&k_decode_attn_mfma<T, G, 3>);
+  }
+  return nullptr;
+}
+
+template <typename T>
+const void* pick_mfma_g(int64_t G, int nb) {
+  switch (G) {
+    case 1: return pick_mfma_nb<T, 1>(nb);
+    case 2: return pick_mfma_nb<T, 2>(nb);
+    case 4: return pick_mfma_nb<T, 4>(nb);
+    case 8: return pick_mfma_nb<T, 8>(nb);
+  }
+  return nullptr;
+}
+
 template <typename T, int G>
 const void* pick_stream(int u) {
   return u == 2 ? reinterpret_cast<const void*>(&k_decode_attn_stream<T, G, 2>)
@@ -864,12 +1217,37 @@ const char* plan_decode_attn(KArgs& a, Launch& l) {
   if (a.n[14] != 1 && a.n[14] != 2) return "decode_attn: position input required";
   if (a.n[25] != a.n[4] || a.n[26] != a.n[4]) return "decode_attn: masks must have the model dtype";
   const int np = static_cast<int>(a.n[28]);
+  if (np == 8) {  // MFMA kernel: one workgroup per (sequence, KV head), n[29] blocks per wave
+    const int nb = static_cast<int>(a.n[29]);
+    if (a.n[4] != F16 && a.n[4] != BF16) return "decode_attn: the MFMA kernel needs a 16-bit cache";
+    if (nb < 1 || nb > 3) return "decode_attn: blocks per wave must be 1, 2 or 3";
+    const int64_t blocks = (C + kMfmaBlock - 1) / kMfmaBlock, waves = (blocks + nb - 1) / nb;
+    if (waves > kMfmaWaves) return "decode_attn: the MFMA kernel covers at most 8 waves of blocks";
+    int e2 = 0;
+    if (!(a.f[0] > 0.f) || std::frexp(a.f[0], &e2) != 0.5f)
+      return "decode_attn: the MFMA kernel needs a power-of-two score divisor";
+    // 32-bit buffer offsets, with room for the last wave's rows past the end
+    const int64_t span = waves * nb * kMfmaBlock;
+    if (a.n[21] < 0 || a.n[23] < 0 || a.n[24] < 0 || span * kHead * 2 > 2147483647 ||
+        span * std::max<int64_t>(a.n[21], a.n[24]) * 2 > 2147483647 ||
+        (H / KV) * a.n[23] * 2 > 2147483647 - span * a.n[24] * 2)
+      return "decode_attn: cache, write mask and mask must span less than 2 GiB per (sequence, KV head)";
+    l.func = a.n[4] == F16 ? pick_mfma_g<__half>(H / KV, nb) : pick_mfma_g<bf16_t>(H / KV, nb);
+    if (!l.func) return "decode_attn: query heads per KV head must be 1, 2, 4 or 8";
+    if (B * KV > 2147483647) return "decode_attn: too many workgroups";
+    l.grid = dim3(static_cast<unsigned>(B * KV));
+    l.block = dim3(static_cast<unsigned>(64 * waves));
+    l.shmem = 0;
+    a.p[kErrPtr] = device_error_word();
+    return nullptr;
+  }
   if (np == 0) {  // streaming kernel: n[29] rows per workgroup, n[30] passes per tile
     const int64_t rpp = a.n[4] == F32 ? 16 : 32, L = a.n[29];
     const int u = static_cast<int>(a.n[30]);
     if (L <= 0 || L % rpp) return "decode_attn: rows per workgroup must be a positive multiple of the rows per pass";
     if (u != 2 && u != 4) return "decode_attn: passes per tile must be 2 or 4";
     if ((C + L - 1) / L > kMaxChunks) return "decode_attn: more than 64 cache ranges per KV head";
+    if ((L + rpp * u - 1) / (rpp * u) > 64) return "decode_attn: more than 64 tiles per workgroup";
     int e2 = 0;
     if (!(a.f[0] > 0.f) || std::frexp(a.f[0], &e2) != 0.5f)
       return "decode_attn: the streaming kernel needs a power-of-two score divisor";
@@ -894,7 +1272,7 @@ const char* plan_decode_attn(KArgs& a, Launch& l) {
     a.p[kErrPtr] = device_error_word();
     return nullptr;
   }
-  if (np != 1 && np != 2 && np != 4) return "decode_attn: passes per workgroup must be 0, 1, 2 or 4";
+  if (np != 1 && np != 2 && np != 4) return "decode_attn: passes per workgroup must be 0, 1, 2, 4 or 8";
   if ((C + (a.n[4] == F32 ? 16 : 32) * np - 1) / ((a.n[4] == F32 ? 16 : 32) * np) > kMaxChunks)
     return "decode_attn: more than 64 cache chunks per KV head";
   switch (a.n[4]) {

@@ -461,9 +461,10 @@ def s_decode_attn(mem, p, n, f):
     mode, length = n[14], n[15]
     cs = n[16:20]
     wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes, stream_rows, unroll = n[20:31]
-    assert passes in (1, 2, 4) or (passes == 0 and stream_rows > 0 and unroll in (2, 4))
+    assert (passes in (1, 2, 4) or (passes == 0 and stream_rows > 0 and unroll in (2, 4))
+            or (passes == 8 and dt in (1, 2) and 1 <= stream_rows <= 3 and -(-C // 32) <= 8 * stream_rows))
     rpp = 16 if dt == 0 else 32
-    chunks = -(-C // stream_rows) if passes == 0 else -(-C // (rpp * passes))
+    chunks = 1 if passes == 8 else -(-C // stream_rows) if passes == 0 else -(-C // (rpp * passes))
     assert chunks <= 64 and (passes != 0 or stream_rows % rpp == 0)
     G = H // KV
     div = _round(np.float32(f[0]), dt)

@@ -24,10 +24,11 @@ def as_float(values):
     return bf16_to_float32(values) if values.dtype == BFLOAT16 else values.astype(np.float32)
 
 
-@pytest.mark.parametrize("passes", [0, 1, 4, "stream8", "stream768"])
+@pytest.mark.parametrize("passes", [0, 1, 4, -2, "stream8", "stream768"])
 @pytest.mark.parametrize("case", attention_cases.CASES, ids=lambda c: c.name)
 def test_decode_attention_matches_oracle(hip, case, passes, monkeypatch):
-    """passes: the chunk kernel's passes per workgroup (0 = chosen), or the
+    """passes: the chunk kernel's passes per workgroup (0 = chosen), -2 the
+    MFMA kernel where it applies (16-bit caches of at most 768 rows), or the
     streaming kernel aiming at 8 workgroups (one or two ranges per KV head,
     many tiles) or 768 (many short ranges, combined)."""
     from chomikgrad import _planner

@@ -267,12 +267,12 @@ def test_memory_plan_reuses_the_arena():
     assert planned.arena_bytes <= 3 * per_value
 
 
-@pytest.mark.parametrize("passes", [0, 1, 2, 4, -1])
+@pytest.mark.parametrize("passes", [0, 1, 2, 4, -1, -2])
 @pytest.mark.parametrize("case", [c for c in attention_cases.CASES if c.C * c.B <= 1000], ids=lambda c: c.name)
 def test_decode_attention_fusion_matches_oracle(case, passes, monkeypatch):
     """The fused decode attention (split over cache chunks, combined by the
-    last workgroup; -1 = the streaming kernel) against the portable chain on
-    the oracle; caches exact."""
+    last workgroup; -1 = the streaming kernel; -2 = the MFMA kernel where it
+    applies) against the portable chain on the oracle; caches exact."""
     from chomikgrad import _planner
 
     monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", passes)
@@ -290,14 +290,22 @@ def test_decode_attention_fusion_matches_oracle(case, passes, monkeypatch):
     (1, 4, 640, 8, 2), (8, 8, 4109, 4, 2), (1, 4, 32768, 8, 2), (2, 2, 70, 2, 4), (1, 1, 1, 1, 2)])
 def test_decode_attention_plan_limits(B, KV, C, G, itemsize, monkeypatch):
     """Every plan covers the cache within the combine's 64 ranges per KV
-    head; the streaming ranges are whole passes; long caches stream."""
+    head; the streaming ranges are whole passes; long caches stream; forced
+    to the MFMA kernel, short 16-bit caches go there, and its at most 8
+    waves hold every 32-row block."""
     from chomikgrad import _planner
 
-    for forced in (0, -1, 1, 4):
+    for forced in (0, -1, -2, 1, 4):
         monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", forced)
         plan = _planner.decode_attention_plan(B, KV, C, G, itemsize)
         rpp = _planner.decode_attention_rows(itemsize)
-        if plan["passes"] == 0:
+        short16 = itemsize == 2 and C <= 768
+        assert (plan["passes"] == 8) == (forced == -2 and short16)
+        if plan["passes"] == 8:
+            assert plan["chunks"] == 1 and 1 <= plan["rows"] <= 3
+            assert -(-C // 32) <= 8 * plan["rows"]
+            assert plan["rows"] == 1 or -(-C // 32) > 8 * (plan["rows"] - 1)
+        elif plan["passes"] == 0:
             assert plan["rows"] % rpp == 0 and plan["unroll"] in (2, 4)
             assert plan["chunks"] == -(-C // plan["rows"])
             assert (plan["chunks"] - 1) * plan["rows"] < C

@@ -78,12 +78,13 @@ def test_c5_speculative_full_shape_equals_greedy(hip):
     fp16 target, 5-token verification blocks, 256-token random prompt, 256
     tokens.  The verification block (multi-row GEMV, generic attention) and
     the single-token decode step compute in different orders, and the top two
-    logits of a random-init model are often within float16 noise, so the two
-    runs may part at such a near-tie.  Checked: the first 32 tokens agree
-    (the decode parity bar), and at the first divergence, if any, the
-    speculative token is greedy decoding's runner-up with a margin within
-    float16 noise -- a driver error (a wrong position, a stale cache row)
-    would pick neither."""
+    logits of a random-init model are sometimes within one float16 ulp (with
+    this seed at generated token 27), so a free-running greedy decode may
+    part from the speculative run at such a tie.  Checked instead, for every
+    one of the 256 tokens: the target's own decode step, fed the speculative
+    tokens (teacher forcing), puts that token at its best logit or within
+    float16 noise of it -- a driver error (a wrong position, a stale cache
+    row, a dropped or repeated token) fails this at some step."""
     print("[gpu case] C5 speculative, full shape", flush=True)
     target_spec, draft_spec = synthetic.TINYLLAMA, synthetic.DRAFT
     target = LlamaRuntime(target_spec.config, synthetic.weights_as_tensors(
@@ -93,28 +94,18 @@ def test_c5_speculative_full_shape_equals_greedy(hip):
     prompt = synthetic.prompt_ids(target_spec.config.vocab_size, 256, seed=0).tolist()
     result = target.generate_speculative(draft, prompt, 256, speculative_tokens=4, bonus=True)
     assert result["generated_tokens"] == 256
-    # plain greedy decoding, recording every step's logits
-    rows = []
-    device = target.device
-    original = device.argmax
-
-    def record(value):
-        rows.append(np.asarray(device.to_numpy(value), dtype=np.float32).reshape(-1))
-        return original(value)
-
-    device.argmax = record
-    try:
-        greedy = target.generate(prompt, 256, loop="reference")["generated_token_ids"]
-    finally:
-        device.argmax = original
     spec = result["generated_token_ids"]
-    assert spec[:32] == greedy[:32]
-    diverged = next((i for i, (a, b) in enumerate(zip(spec, greedy)) if a != b), None)
-    if diverged is not None:
-        logits = rows[diverged]
-        order = np.argsort(-logits, kind="stable")
-        assert spec[diverged] == int(order[1]), "speculative token is not greedy's runner-up"
-        margin = float(logits[order[0]] - logits[order[1]])
-        assert margin <= 0.02, f"divergence at a margin of {margin}"
+    # the target's greedy decode steps, fed the speculative tokens
+    context = len(prompt) + 256
+    logits, caches = target.prefill(prompt, context)
+    gaps = []
+    for i, token in enumerate(spec):
+        row = np.asarray(target.device.to_numpy(logits), dtype=np.float32).reshape(-1)
+        gaps.append(float(row.max() - row[token]))
+        if i + 1 < len(spec):
+            logits, caches = target._decode_step(token, len(prompt) + i, context, caches)
+    worst = int(np.argmax(gaps))
+    assert gaps[worst] <= 0.02, f"token {worst} ({spec[worst]}) trails the best logit by {gaps[worst]}"
+    ties = [i for i, g in enumerate(gaps) if g > 0]
     print(f"C5: {result['warm_tokens_per_second']:.1f} tok/s, acceptance {result['acceptance_rate']:.3f}, "
-          f"{result['target_verification_calls']} verification blocks, first divergence {diverged}", flush=True)
+          f"{result['target_verification_calls']} verification blocks, near-tie picks at {ties}", flush=True)

@@ -40,12 +40,14 @@ from .lazy import GraphPlan, LazyNode, Op
 K_FILL, K_COPY, K_ELEMENTWISE, K_REDUCE, K_GATHER, K_MATMUL, K_SOFTMAX = 1, 2, 3, 4, 5, 6, 7
 K_RMSNORM, K_ROPE, K_SDPA, K_KV_WRITE, K_KV_PLACE, K_GEMV, K_GEMM = 8, 9, 10, 11, 12, 13, 14
 K_DECODE_ATTN = 17
+K_ATTN_PROJ = 18
 
 KIND_NAMES = {
     K_FILL: "fill", K_COPY: "copy", K_ELEMENTWISE: "fused_elementwise",
     K_REDUCE: "reduce", K_GATHER: "gather", K_MATMUL: "matmul", K_SOFTMAX: "softmax",
     K_RMSNORM: "rms_norm", K_ROPE: "rope", K_SDPA: "sdpa", K_KV_WRITE: "kv_write",
     K_KV_PLACE: "kv_place", K_GEMV: "gemv", K_GEMM: "gemm", K_DECODE_ATTN: "decode_attention",
+    K_ATTN_PROJ: "attn_proj",
 }
 
 OPCODES = {"add": 1, "sub": 2, "mul": 3, "div": 4, "equal": 5, "neg": 6, "exp": 7,
@@ -76,6 +78,14 @@ DECODE_ATTN_STREAM_UNROLL = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_UNROLL", 
 # tiles one streaming workgroup may cover (it flags tiles with blended rows
 # in a 64-bit mask)
 DECODE_ATTN_STREAM_MAX_TILES = 64
+# Batch-1 decode, opt-in: the chunk attention stores only its partials and
+# the output projection (the next GEMV) combines them instead of the
+# attention's own cross-workgroup ticket and combine.  Measured at the C2
+# shape it loses (attention 8.9 -> 5.6 us, but the projection 4.0 -> 8.2 us:
+# each block reads every head's partials, 169 KB, before its dot products),
+# so it is off by default.
+ATTN_PROJ_FUSE = int(os.environ.get("CHOMIK_HIP_ATTN_PROJ", "0"))
+ATTN_PROJ_MAX_CHUNKS = 32
 # The MFMA kernel: one workgroup of at most 8 waves per (sequence, KV head),
 # each wave with 1-3 blocks of 32 cache rows in registers.
 DECODE_ATTN_MFMA_BLOCK = 32
@@ -1237,6 +1247,47 @@ def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitte
     return [s for s in steps if id(s) not in removed]
 
 
+def fuse_attention_projection(steps: List[Step], outputs: List[PV]) -> List[Step]:
+    """Batch-1 chunk decode attention whose output feeds only the next
+    single-row GEMV (the o projection, residual epilogue or none) -> the
+    attention stores its per-chunk partials only and a K_ATTN_PROJ step
+    combines them while its weight rows stream (the attention's own combine
+    needs a cross-workgroup ticket and three memory round trips)."""
+    if not ATTN_PROJ_FUSE:
+        return steps
+    counts = _consumers(steps, outputs)
+    for index, att in enumerate(steps):
+        if att.kind != K_DECODE_ATTN or att.attrs["passes"] not in (1, 2, 4):
+            continue
+        q, partials = att.ins[0], att.ins[10]
+        out = att.outs[0]
+        B, H = q.shape[0], q.shape[1]
+        C = att.ins[5].shape[2]
+        chunks = -(-C // (decode_attention_rows(q.itemsize) * att.attrs["passes"]))
+        if B != 1 or q.itemsize != 2 or H * 64 not in (1024, 2048) or not 2 <= chunks <= ATTN_PROJ_MAX_CHUNKS:
+            continue
+        if not out.whole() or counts.get(id(out.storage)) != 1:
+            continue
+        users = [(i, s) for i, s in enumerate(steps) if any(pv.storage is out.storage for pv in s.reads())]
+        if len(users) != 1:
+            continue
+        at, proj = users[0]
+        if (proj.kind != K_GEMV or proj.attrs["silu"] or proj.attrs["prologue"] is not None
+                or proj.attrs["rows"] != 1 or proj.attrs["K"] != H * 64 or len(proj.attrs["segments"]) != 1
+                or proj.attrs.get("workspace") is not None or not proj.ins[0].same_data(out)):
+            continue
+        seg = proj.attrs["segments"][0]
+        w, res, y = seg["w"], seg["res"], seg["out"]
+        if not (w.contiguous() and w.dtype == q.dtype and (w.offset * w.itemsize) % 16 == 0
+                and y.contiguous() and y.dtype == q.dtype
+                and (res is None or (res.contiguous() and res.dtype == q.dtype))):
+            continue
+        att.attrs["partials_only"] = True
+        steps[at] = Step(K_ATTN_PROJ, [partials, w, res], [y],
+                         {"N": w.shape[0], "K": H * 64, "H": H, "chunks": chunks})
+    return steps
+
+
 GEMM_SEGMENT_WIDTH = 128  # segment widths of a merged GEMM: whole 128-column tiles
 
 
@@ -1496,10 +1547,15 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
                 v.strides[0], v.strides[1], v.strides[3],
                 a["mode"], a["table_length"]] + list(cache_k.strides)
         ints += [ws[0], ws[2], ms[0], ms[1], ms[3], dtype_code(mask.dtype), dtype_code(w.dtype),
-                 1 if a["in_place"] else 0, a["passes"], a["stream_rows"], a["unroll"]]
+                 1 if a["in_place"] else 0, a["passes"], a["stream_rows"], a["unroll"],
+                 1 if a.get("partials_only") else 0]
         ptrs = [_ptr(pv) for pv in (q, k, v, position, table, cache_k, cache_v, w, mask, out, out_k, out_v,
                                     tickets, partials)]
         return kind, ptrs, ints, [a["divisor"]]
+    if kind == K_ATTN_PROJ:
+        partials, w, res = step.ins
+        ptrs = [_ptr(partials), _ptr(w), _ptr(res), _ptr(step.outs[0])]
+        return kind, ptrs, [a["N"], a["K"], a["H"], a["chunks"], dtype_code(w.dtype)], []
     if kind == K_GEMM:
         x, w = step.ins[0], step.ins[1]
         out = step.outs[0]
@@ -1625,6 +1681,7 @@ def plan_graph(compiler, outputs: Sequence[LazyNode], dynamic_inputs: Sequence[L
     steps = merge_sibling_gemvs(steps)
     steps = merge_sibling_gemms(steps)
     steps = fuse_decode_attention(steps, out_pvs, emitter)
+    steps = fuse_attention_projection(steps, out_pvs)
     steps = attach_gemv_workspace(steps, emitter)
 
     # Program outputs: leaves are returned as they are, whole intermediates

@@ -192,8 +192,10 @@ __device__ __forceinline__ void combine_chunks(const KArgs& a, int64_t b, int64_
 // (1 scalar, 2 per sequence), n[15] table length, n[16..19] cache strides
 // (b, g, c, d) (same for K and V), n[20..21] w strides (b, c), n[22..24]
 // mask strides (b, h, c), n[25] mask dtype, n[26] w dtype (both must be the
-// model dtype), n[27] in place, n[28] passes per workgroup NP (1, 2 or 4);
-// f[0] score divisor (sqrt(hd) before rounding).
+// model dtype), n[27] in place, n[28] passes per workgroup NP (1, 2 or 4),
+// n[31] partials only (with NS > 1: the next step, the output projection,
+// combines them and p[9] is not written); f[0] score divisor (sqrt(hd) before
+// rounding).
 template <typename T, int G, int NP>
 __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
   using E = Elem<T>;
@@ -445,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
     reinterpret_cast<uint4*>(Ko + dst)[part] = kvec;
     reinterpret_cast<uint4*>(Vo + dst)[part] = vvec;
   }
-  if (NS == 1) return;
+  if (NS == 1 || a.n[31] != 0) return;  // n[31]: the output projection combines
   combine_chunks<T, G>(a, b, g, NS);
 }
 
@@ -932,7 +934,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void k_decode_attn_mfma(KArgs a) {
   __shared__ float wmax[kMfmaWaves][16], wsum[kMfmaWaves][16];
   __shared__ float wacc[kMfmaWaves][G][kHead];
 
-  const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
+  const int64_t H = a.n[1], KV = a.n[2], C = a.n[3];
   const int64_t b = blockIdx.x / KV, g = blockIdx.x % KV;
   const int dt = E::code;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1273,6 +1275,8 @@ const char* plan_decode_attn(KArgs& a, Launch& l) {
     return nullptr;
   }
   if (np != 1 && np != 2 && np != 4) return "decode_attn: passes per workgroup must be 0, 1, 2, 4 or 8";
+  if (a.n[31] != 0 && (C + (a.n[4] == F32 ? 16 : 32) * np - 1) / ((a.n[4] == F32 ? 16 : 32) * np) < 2)
+    return "decode_attn: partials only needs at least two chunks";
   if ((C + (a.n[4] == F32 ? 16 : 32) * np - 1) / ((a.n[4] == F32 ? 16 : 32) * np) > kMaxChunks)
     return "decode_attn: more than 64 cache chunks per KV head";
   switch (a.n[4]) {

@@ -1124,6 +1124,145 @@ const void* pick_mfma(int ks, bool silu) {
   }
 }
 
+// Output projection of a split-context decode attention (batch 1): the
+// attention launch leaves its per-chunk partials -- for every head h and
+// chunk k the unnormalised P V row O[h][k][0..63], the maximum m[h][k] and
+// the exp-sum l[h][k] -- and this kernel combines them into the attention
+// output x (the arithmetic of the attention kernel's own combine:
+// f_k = exp(m_k - max m), x = round(sum_k O_k f_k / sum_k l_k f_k)) and
+// computes y = round(r + round(W x)) (residual r, or y = round(W x)).  Each
+// wave owns one output row; its weight row and residual are issued first,
+// so they stream while the block combines x into LDS.  This removes the
+// attention's cross-workgroup ticket and combine (three memory round trips)
+// from the decode chain.
+// p[0] partials (float32: H*NS*64 sums, H*NS maxima, H*NS exp-sums),
+// p[1] W (N, K) row-major, p[2] residual (N) or null, p[3] out (N).
+// n[0] N, n[1] K = 64 H, n[2] H, n[3] NS (2..32), n[4] dtype.
+constexpr int kProjWaves = 16;   // output rows per block
+constexpr int kProjChunks = 32;  // chunks per head at most
+constexpr int kProjHeads = 32;   // heads at most (K <= 2048)
+
+__device__ __forceinline__ float proj_nan_max(float a, float b) { return (b != b || b > a) ? b : a; }
+
+template <typename T, int VPL>
+__global__ __launch_bounds__(64 * kProjWaves) void k_attn_proj(KArgs a) {
+  using E = Elem<T>;
+  using W = Word<T>;
+  constexpr int kHead = 64;
+  constexpr int kThreads = 64 * kProjWaves;
+  constexpr int QT = VPL * 8 * 64 / kThreads;  // combined values per thread (K = 512 VPL)
+  constexpr int HW = (VPL * 8 + kProjWaves - 1) / kProjWaves;  // heads per wave (H = 8 VPL)
+  __shared__ float fac[kProjHeads][kProjChunks];
+  __shared__ __attribute__((aligned(16))) T xs[kProjHeads * kHead];
+
+  const int64_t N = a.n[0], K = a.n[1], H = a.n[2], NS = a.n[3];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x * int64_t(kProjWaves) + wave;
+  const int64_t rr = row < N ? row : N - 1;
+
+  // -- this wave's weight row and residual (no wait before they are issued)
+  const T* Wm = static_cast<const T*>(a.p[1]);
+  const uint4* wrow = reinterpret_cast<const uint4*>(Wm + rr * K);
+  uint4 wv[VPL];
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) wv[u] = load_w<true>(wrow + lane + 64 * u);
+  const T* R = static_cast<const T*>(a.p[2]);
+  const float resv = E::to_f(R ? R[rr] : Wm[0]);  // without a residual: read and discarded
+
+  // -- the partials: per head the chunk maxima and exp-sums (one wave per
+  // head, one lane per chunk), then this thread's P V sums; every load is
+  // issued before the first use, chunk indices clamped (extra terms get 0)
+  const float* P = static_cast<const float*>(a.p[0]);
+  const int64_t total = H * NS;
+  const int nlast = static_cast<int>(NS) - 1;
+  const int kc = lane < nlast ? lane : nlast;
+  float mk_[HW], lk_[HW];
+#pragma unroll
+  for (int x = 0; x < HW; ++x) {
+    const int64_t h = wave + int64_t(kProjWaves) * x;
+    const int64_t at = (h < H ? h : 0) * NS + kc;
+    mk_[x] = P[total * kHead + at];
+    lk_[x] = P[total * (kHead + 1) + at];
+  }
+  float ov[QT][kProjChunks];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;  // x index: head i / 64, dim i % 64
+    const float* Op = P + (int64_t(i / kHead) * NS) * kHead + (i % kHead);
+#pragma unroll
+    for (int k0 = 0; k0 < kProjChunks; k0 += 8) {
+      if (k0 >= NS) break;  // uniform: only the blocks of 8 chunks that exist
+#pragma unroll
+      for (int k = k0; k < k0 + 8; ++k) ov[t][k] = Op[(k < nlast ? k : nlast) * kHead];
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < HW; ++x) {
+    const int64_t h = wave + int64_t(kProjWaves) * x;
+    if (h >= H) break;
+    const float mk = lane < NS ? mk_[x] : -INFINITY;
+    float m = mk;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = proj_nan_max(m, __shfl_xor(m, o, 64));
+    const float f = lane < NS ? __expf(mk - m) : 0.f;
+    float l = lane < NS ? lk_[x] * f : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    if (lane < kProjChunks) fac[h][lane] = f / l;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int i = tid + kThreads * t;
+    const float* F = fac[i / kHead];
+    float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k0 = 0; k0 < kProjChunks; k0 += 8) {
+      if (k0 >= NS) break;
+#pragma unroll
+      for (int k = k0; k < k0 + 8; ++k) o4[k & 3] = fmaf(ov[t][k], k < NS ? F[k] : 0.f, o4[k & 3]);
+    }
+    xs[i] = E::from_f((o4[0] + o4[1]) + (o4[2] + o4[3]));
+  }
+  __syncthreads();
+
+  // -- y = W x for this wave's row: the row GEMV's lane layout and order
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < VPL; ++u) {
+    const uint4 xv = reinterpret_cast<const uint4*>(xs)[lane + 64 * u];
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = W::dot(xw[i], ww[i], acc);
+  }
+  acc = wave_sum(acc);
+  float y = E::round(acc);
+  y = R ? E::round(resv + y) : y;
+  if (lane == 0 && row < N) static_cast<T*>(a.p[3])[row] = E::from_f(y);
+}
+
+const char* plan_attn_proj(KArgs& a, Launch& l) {
+  const int64_t N = a.n[0], K = a.n[1], H = a.n[2], NS = a.n[3];
+  const int dt = static_cast<int>(a.n[4]);
+  if (dt != F16 && dt != BF16) return "attn_proj: float16 or bfloat16 required";
+  if (N <= 0 || H <= 0 || K != 64 * H) return "attn_proj: K must be 64 per head";
+  if (NS < 2 || NS > kProjChunks) return "attn_proj: 2..32 chunks per head";
+  switch (K) {
+    case 1024: l.func = dt == F16 ? reinterpret_cast<const void*>(&k_attn_proj<__half, 2>)
+                                  : reinterpret_cast<const void*>(&k_attn_proj<bf16_t, 2>); break;
+    case 2048: l.func = dt == F16 ? reinterpret_cast<const void*>(&k_attn_proj<__half, 4>)
+                                  : reinterpret_cast<const void*>(&k_attn_proj<bf16_t, 4>); break;
+    default: return "attn_proj: K must be 1024 or 2048";
+  }
+  const int64_t blocks = (N + kProjWaves - 1) / kProjWaves;
+  if (blocks > 2147483647) return "attn_proj: too many rows";
+  l.grid = dim3(static_cast<unsigned>(blocks));
+  l.block = dim3(64 * kProjWaves);
+  l.shmem = 0;
+  return nullptr;
+}
+
 const char* plan_gemv(KArgs& a, Launch& l) {
   const int64_t M = a.n[0], K = a.n[1];
   const int dt = static_cast<int>(a.n[3]);
@@ -1247,5 +1386,6 @@ const char* plan_gemv(KArgs& a, Launch& l) {
 }  // namespace
 
 CHIP_REGISTER_KIND(CHIP_K_GEMV, plan_gemv);
+CHIP_REGISTER_KIND(CHIP_K_ATTN_PROJ, plan_attn_proj);
 
 }  // namespace chip

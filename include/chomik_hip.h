@@ -62,7 +62,8 @@ enum chip_kind {
   CHIP_K_GEMM = 14,
   CHIP_K_ARGMAX = 15,
   CHIP_K_FLASH = 16,
-  CHIP_K_DECODE_ATTN = 17
+  CHIP_K_DECODE_ATTN = 17,
+  CHIP_K_ATTN_PROJ = 18
 };
 
 typedef struct chip_info {

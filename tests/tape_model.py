@@ -426,6 +426,28 @@ def s_gemv(mem, p, n, f):
     return 0
 
 
+def s_attn_proj(mem, p, n, f):
+    """Combine of the decode attention's partials (batch 1), then the output
+    projection y = round(r + round(W x)) of the combined x."""
+    N, K, H, NS, dt = n[0:5]
+    assert K == 64 * H and 2 <= NS <= 32
+    total = H * NS
+    parts = mem.view(p[0], 0, total * 66).astype(np.float64)
+    O = parts[:total * 64].reshape(H, NS, 64)
+    m = parts[total * 64:total * 65].reshape(H, NS)
+    s = parts[total * 65:].reshape(H, NS)
+    with np.errstate(all="ignore"):
+        f = np.exp(m - m.max(axis=1, keepdims=True))
+        fac = f / (s * f).sum(axis=1, keepdims=True)
+        x = _round((O * fac[:, :, None]).sum(axis=1).astype(np.float32), dt).reshape(1, K)
+        W = load(mem, p[1], dt, np.arange(N)[:, None] * K + np.arange(K)[None, :])
+        y = _round((x.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32), dt)
+        if p[2][0] >= 0:
+            y = _round(load(mem, p[2], dt, np.arange(N)[None, :]) + y, dt)
+    store(mem, p[3], dt, np.arange(N), y.reshape(-1))
+    return 0
+
+
 def s_gemm(mem, p, n, f):
     M, N, K, dt, lda, ldw, ldc, ldr, silu, ldwu, has_res = n[0:11]
     A = load(mem, p[0], dt, np.arange(M)[:, None] * lda + np.arange(K)[None, :])
@@ -460,12 +482,21 @@ def s_decode_attn(mem, p, n, f):
     qs, ks, vs = n[5:8], n[8:11], n[11:14]
     mode, length = n[14], n[15]
     cs = n[16:20]
-    wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes, stream_rows, unroll = n[20:31]
+    wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes, stream_rows, unroll, partials_only = n[20:32]
     assert (passes in (1, 2, 4) or (passes == 0 and stream_rows > 0 and unroll in (2, 4))
             or (passes == 8 and dt in (1, 2) and 1 <= stream_rows <= 3 and -(-C // 32) <= 8 * stream_rows))
     rpp = 16 if dt == 0 else 32
     chunks = 1 if passes == 8 else -(-C // stream_rows) if passes == 0 else -(-C // (rpp * passes))
     assert chunks <= 64 and (passes != 0 or stream_rows % rpp == 0)
+    assert not partials_only or (passes in (1, 2, 4) and chunks >= 2 and B == 1)
+    if partials_only:
+        # partials that combine to the output: chunk 0 holds it with maximum
+        # 0 and exp-sum 1, the other chunks maximum -inf and exp-sum 0
+        total = H * chunks
+        parts = mem.view(p[13], 0, total * 66)
+        parts[:] = 0.0
+        parts[total * 64:total * 65].reshape(H, chunks)[:, 1:] = -np.inf
+        parts[total * 65:total * 66].reshape(H, chunks)[:, 0] = 1.0
     G = H // KV
     div = _round(np.float32(f[0]), dt)
     error = 0
@@ -501,7 +532,10 @@ def s_decode_attn(mem, p, n, f):
                     # float32 softmax and P V (one division, one rounding)
                     e = np.exp(sc.astype(np.float64) - np.float64(sc.max()))
                     out = ((e @ Vn.astype(np.float64)) / e.sum()).astype(np.float32)
-                    store(mem, p[9], dt, (b * H + h) * 64 + d, out)
+                    if partials_only:
+                        parts[(h * chunks) * 64 + d] = out
+                    else:
+                        store(mem, p[9], dt, (b * H + h) * 64 + d, out)
     for (b, g), (idx, Kn, Vn, w) in newk.items():
         if in_place:
             rows = w != 0
@@ -518,5 +552,5 @@ STEP = {
     P.K_FILL: s_fill, P.K_COPY: s_copy, P.K_ELEMENTWISE: s_elementwise, P.K_REDUCE: s_reduce,
     P.K_GATHER: s_gather, P.K_MATMUL: s_matmul, P.K_SOFTMAX: s_softmax, P.K_RMSNORM: s_rmsnorm,
     P.K_ROPE: s_rope, P.K_SDPA: s_sdpa, P.K_KV_WRITE: s_kv_write, P.K_KV_PLACE: s_kv_place,
-    P.K_GEMV: s_gemv, P.K_GEMM: s_gemm, P.K_DECODE_ATTN: s_decode_attn,
+    P.K_GEMV: s_gemv, P.K_GEMM: s_gemm, P.K_DECODE_ATTN: s_decode_attn, P.K_ATTN_PROJ: s_attn_proj,
 }

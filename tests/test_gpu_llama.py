@@ -14,6 +14,7 @@ from chomikgrad.llama import (
     LlamaBatchedDecoderStep,
     LlamaConfig,
     LlamaDecoderBlock,
+    LlamaDecoderStep,
     LlamaForCausalLM,
     _rope_rotations,
     block_masks,
@@ -164,3 +165,43 @@ def test_batched_bf16_decode_matches_emulated_oracle(hip):
     np.testing.assert_allclose(bf16_to_float32(got[0]), bf16_to_float32(expected[0]), atol=3e-2, rtol=3e-2)
     for g, e in zip(got[1:], expected[1:]):
         np.testing.assert_allclose(bf16_to_float32(g), bf16_to_float32(e), atol=3e-2, rtol=3e-2)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+def test_attention_partials_combined_by_output_projection(hip, dtype, monkeypatch):
+    """Batch-1 decode layer with 16 heads of 64 over a 100-row cache (4
+    chunks): the attention stores partials only and the output projection
+    (K_ATTN_PROJ) combines them; the same layer with the fusion off combines
+    in the attention.  Both match the oracle; the caches are exact; the two
+    hip programs agree to the last bit (the same combine and row-GEMV
+    arithmetic)."""
+    from chomikgrad import _planner
+
+    announce(f"attention partials combined by the output projection {np.dtype(dtype).name}")
+    config = LlamaConfig(vocab_size=256, hidden_size=1024, intermediate_size=512, num_hidden_layers=1,
+                         num_attention_heads=16, num_key_value_heads=4, max_position_embeddings=128)
+    weights = synthetic.weights_as_tensors(synthetic.host_weights(config, dtype, seed=11))
+    C, position = 100, 77
+    rng = np.random.default_rng(8)
+    caches = [Tensor((rng.normal(size=(1, 4, C, 64)) * 0.5).astype(np.float32), dtype=dtype) for _ in range(2)]
+    attention, write = decode_masks(position, C, dtype)
+    leaves = [Tensor(np.array([[17]], np.int32), copy=False),
+              Tensor(_rope_rotations(1, 64, config.rope_theta, dtype, offset=position), copy=False),
+              Tensor(attention, copy=False), Tensor(write, copy=False),
+              Tensor(np.asarray(position, np.int32), copy=False)]
+    dec = LlamaDecoderStep(config, weights, cache_length=C, dtype=dtype)
+    outputs = dec(*leaves[:4], [(caches[0], caches[1])], position=leaves[4])
+    expected = realize(*outputs, compiler="cpu")
+    got = {}
+    for fuse in (1, 0):
+        monkeypatch.setattr(_planner, "ATTN_PROJ_FUSE", fuse)
+        hip.close()  # drop programs cached by signature: plan again with the knob
+        program = compile_graph(*outputs, compiler="hip")
+        assert ("attn_proj" in program.source) == bool(fuse)
+        values = [hip.device.to_numpy(v) for v in program.run(synchronize=True)]
+        as_float = (lambda v: bf16_to_float32(v)) if dtype is BFLOAT16 else (lambda v: np.asarray(v, np.float32))
+        np.testing.assert_allclose(as_float(values[0]), as_float(expected[0]), atol=FP16_ATOL, rtol=FP16_RTOL)
+        for value, reference in zip(values[1:], expected[1:]):
+            np.testing.assert_array_equal(np.asarray(value).view(np.uint8), np.asarray(reference).view(np.uint8))
+        got[fuse] = values[0]
+    np.testing.assert_array_equal(np.asarray(got[1]).view(np.uint8), np.asarray(got[0]).view(np.uint8))

@@ -147,6 +147,44 @@ def test_fp16_decode_step_matches_oracle_roundings():
         assert np.mean(value == reference) > 0.99
 
 
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16])
+def test_attention_partials_combined_by_output_projection(dtype, monkeypatch):
+    """Batch-1 decode with 16 heads of 64 over a 100-row cache (4 chunks):
+    the attention stores its partials only and the output projection
+    combines them (K_ATTN_PROJ, residual epilogue); with the fusion off the
+    attention combines itself.  Both match the oracle's portable graph."""
+    from chomikgrad import _planner
+
+    config = LlamaConfig(vocab_size=256, hidden_size=1024, intermediate_size=512, num_hidden_layers=1,
+                         num_attention_heads=16, num_key_value_heads=4, max_position_embeddings=128)
+    weights = synthetic.weights_as_tensors(synthetic.host_weights(config, dtype, seed=11))
+    C, position = 100, 77
+    rng = np.random.default_rng(8)
+    caches = [Tensor((rng.normal(size=(1, 4, C, 64)) * 0.5).astype(np.float32), dtype=dtype) for _ in range(2)]
+    attention, write = decode_masks(position, C, dtype)
+    leaves = [Tensor(np.array([[17]], np.int32), copy=False),
+              Tensor(_rope_rotations(1, 64, config.rope_theta, dtype, offset=position), copy=False),
+              Tensor(attention, copy=False), Tensor(write, copy=False),
+              Tensor(np.asarray(position, np.int32), copy=False)]
+    dec = LlamaDecoderStep(config, weights, cache_length=C, dtype=dtype)
+    outputs = dec(*leaves[:4], [(caches[0], caches[1])], position=leaves[4])
+    expected = realize(*outputs, compiler="cpu")
+    results = {}
+    for fuse in (1, 0):
+        monkeypatch.setattr(_planner, "ATTN_PROJ_FUSE", fuse)
+        planned, got = model_run(outputs, leaves + caches)
+        kinds = [s.kind for s in planned.steps]
+        assert kinds.count(_planner.K_ATTN_PROJ) == fuse
+        attn = next(s for s in planned.steps if s.kind == K_DECODE_ATTN)
+        assert bool(attn.attrs.get("partials_only")) == bool(fuse)
+        np.testing.assert_allclose(as_float(got[0]), as_float(expected[0]), atol=2e-2, rtol=1e-2)
+        for value, reference in zip(got[1:], expected[1:]):  # the caches: exact
+            np.testing.assert_array_equal(np.asarray(value).view(np.uint8), np.asarray(reference).view(np.uint8))
+        results[fuse] = got[0]
+    # the fused projection computes the same values as the unfused chain
+    np.testing.assert_allclose(as_float(results[1]), as_float(results[0]), atol=1e-2, rtol=1e-2)
+
+
 def test_prefill_with_cache_placement():
     config = synthetic.TINY.config
     weights = tiny_weights(config, 9)

@@ -1496,8 +1496,12 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
     if kind == K_ROPE:
         x, position, table = step.ins
         out = step.outs[0]
+        # 16-byte aligned rows of x, the table and the output (vector kernel)
+        aligned = (x.strides[3] == 1 and all(s % 8 == 0 for s in x.strides[:3])
+                   and all(pv.offset % 8 == 0 for pv in (x, table, out)) and table.contiguous())
         return kind, [_ptr(x), _ptr(position), _ptr(table), _ptr(out)], (
-            list(x.shape) + list(x.strides) + [dtype_code(x.dtype), a["mode"], a["offset"], a["table_length"]]
+            list(x.shape) + list(x.strides) + [dtype_code(x.dtype), a["mode"], a["offset"], a["table_length"],
+                                               1 if aligned else 0]
         ), []
     if kind == K_SDPA:
         q, k, v, mask = step.ins

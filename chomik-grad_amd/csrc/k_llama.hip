@@ -117,7 +117,8 @@ const char* plan_rmsnorm(KArgs& a, Launch& l) {
 // p[0] x, p[1] positions (int32 or null), p[2] table (len, 2, h), p[3] out.
 // n[0] B, n[1] H, n[2] T, n[3] hd, n[4..7] x strides (b, h, t, d), n[8]
 // dtype, n[9] mode (0: offset + t, 1: scalar position + offset + t,
-// 2: position[b] + offset + t), n[10] offset, n[11] table length.
+// 2: position[b] + offset + t), n[10] offset, n[11] table length, n[12]
+// rows of x, table and out 16-byte aligned with unit stride along the row.
 __global__ void k_rope(KArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -147,10 +148,59 @@ __global__ void k_rope(KArgs a) {
   }
 }
 
+// 16-bit rows of 64 elements, unit stride along the row and 16-byte aligned
+// (n[12] = 1): four lanes per row, lane j rotating dims 8j .. 8j + 7 with
+// their partners 32 + 8j .. 32 + 8j + 7 in 16-byte vectors (k_rope keeps one
+// wave per row and half its lanes idle).  Same arithmetic and rounding.
+template <typename T>
+__global__ __launch_bounds__(256) void k_rope_vec(KArgs a) {
+  const int64_t B = a.n[0], H = a.n[1], T_ = a.n[2];
+  const int64_t gid = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  const int64_t row = gid >> 2;
+  const int j = static_cast<int>(gid & 3);
+  if (row >= B * H * T_) return;  // no barrier in this kernel
+  const int64_t t = row % T_, h = (row / T_) % H, b = row / (T_ * H);
+  int64_t pos = a.n[10] + t;
+  if (a.n[9] == 1) pos += static_cast<const int32_t*>(a.p[1])[0];
+  if (a.n[9] == 2) pos += static_cast<const int32_t*>(a.p[1])[b];
+  const bool ok = pos >= 0 && pos < a.n[11];
+  if (!ok && j == 0) raise_error(a, ERR_POSITION);
+  float o1[8], o2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o1[e] = o2[e] = 0.f;
+  if (ok) {
+    const T* X = static_cast<const T*>(a.p[0]) + b * a.n[4] + h * a.n[5] + t * a.n[6] + 8 * j;
+    const T* tab = static_cast<const T*>(a.p[2]) + pos * 64 + 8 * j;
+    float x1[8], x2[8], c[8], s[8];
+    unpack<T>(*reinterpret_cast<const uint4*>(X), x1);
+    unpack<T>(*reinterpret_cast<const uint4*>(X + 32), x2);
+    unpack<T>(*reinterpret_cast<const uint4*>(tab), c);
+    unpack<T>(*reinterpret_cast<const uint4*>(tab + 32), s);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o1[e] = __fadd_rn(__fmul_rn(x1[e], c[e]), __fmul_rn(x2[e], -s[e]));
+      o2[e] = __fadd_rn(__fmul_rn(x1[e], s[e]), __fmul_rn(x2[e], c[e]));
+    }
+  }
+  T* out = static_cast<T*>(a.p[3]) + row * 64 + 8 * j;
+  *reinterpret_cast<uint4*>(out) = pack<T>(o1);
+  *reinterpret_cast<uint4*>(out + 32) = pack<T>(o2);
+}
+
 const char* plan_rope(KArgs& a, Launch& l) {
   if (a.n[0] <= 0 || a.n[1] <= 0 || a.n[2] <= 0 || a.n[3] <= 0 || (a.n[3] & 1)) return "rope: bad shape";
   if (a.n[9] < 0 || a.n[9] > 2) return "rope: bad position mode";
   const int64_t rows = a.n[0] * a.n[1] * a.n[2];
+  const int dt = static_cast<int>(a.n[8]);
+  if ((dt == F16 || dt == BF16) && a.n[3] == 64 && a.n[7] == 1 && a.n[12] == 1) {
+    if (rows * 4 / 256 + 1 > 2147483647) return "rope: too many rows";
+    l.func = dt == F16 ? reinterpret_cast<const void*>(&k_rope_vec<__half>)
+                       : reinterpret_cast<const void*>(&k_rope_vec<bf16_t>);
+    l.grid = dim3(static_cast<unsigned>((rows * 4 + 255) / 256));
+    l.block = dim3(256);
+    a.p[kErrPtr] = device_error_word();
+    return nullptr;
+  }
   l.func = reinterpret_cast<const void*>(&k_rope);
   l.grid = dim3(static_cast<unsigned>((rows + 3) / 4));
   l.block = dim3(256);

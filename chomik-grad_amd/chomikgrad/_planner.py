@@ -75,9 +75,6 @@ DECODE_ATTN_MAX_CHUNKS = 64
 DECODE_ATTN_STREAM_ABOVE = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_ABOVE", "768"))
 DECODE_ATTN_STREAM_WGS = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_WGS", "768"))
 DECODE_ATTN_STREAM_UNROLL = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_UNROLL", "2"))
-# tiles one streaming workgroup may cover (it flags tiles with blended rows
-# in a 64-bit mask)
-DECODE_ATTN_STREAM_MAX_TILES = 64
 # Batch-1 decode, opt-in: the chunk attention stores only its partials and
 # the output projection (the next GEMV) combines them instead of the
 # attention's own cross-workgroup ticket and combine.  Measured at the C2
@@ -1169,12 +1166,10 @@ def decode_attention_plan(B: int, KV: int, C: int, G: int, itemsize: int, diviso
     if not stream:
         passes = decode_attention_passes(B, KV, C, itemsize)
         return {"passes": passes, "chunks": -(-C // (rpp * passes)), "rows": 0, "unroll": 0}
-    unroll = DECODE_ATTN_STREAM_UNROLL
     target = max(1, min(DECODE_ATTN_MAX_CHUNKS, -(-DECODE_ATTN_STREAM_WGS // (B * KV))))
-    # a workgroup streams at most DECODE_ATTN_STREAM_MAX_TILES tiles
-    target = min(DECODE_ATTN_MAX_CHUNKS, max(target, -(-C // (DECODE_ATTN_STREAM_MAX_TILES * rpp * unroll))))
     rows = -(-C // target)
     rows = -(-rows // rpp) * rpp
+    unroll = DECODE_ATTN_STREAM_UNROLL
     return {"passes": 0, "chunks": -(-C // rows), "rows": rows, "unroll": unroll}
 
 

@@ -503,21 +503,21 @@ __device__ __forceinline__ uint4 buffer_row(__amdgpu_buffer_rsrc_t r, int off) {
 // short caches its one latency chain is the kernel's time, but a long cache
 // becomes thousands of workgroups that run in several latency-bound rounds.
 // Here a workgroup owns a range of L rows (n[29], a multiple of the rows per
-// pass, at most 64 tiles; NS = ceil(C / L) ranges per (sequence, KV head))
-// and streams it in tiles of U passes.  Two register sets alternate, so two
-// tiles of K and V (with their write-mask and mask values) are in flight
-// while one is scored and accumulated: tile t + 2 is loaded into the set
-// that tile t has just left.  Loads are buffer loads at loop-invariant 32-bit
-// offsets plus the tile's offset; rows past the cache read 0, and the loads
-// past the last tile use an out-of-range offset (zeros, no memory traffic),
-// so the loop has no peeled tail.  Each row group (the LPR lanes sharing a
-// row) keeps an online softmax per query head -- running maximum and
-// exp-sum, rescaled once per tile -- and its lanes' slices of P V in
-// registers, so V is never staged in LDS.  The main pass leaves out the rows
-// with w != 0 (in place: only the new token's row); a tile holding any is
-// flagged, the first one per wave kept in LDS, and after the loop those rows
-// are blended, written to the cache, scored and accumulated.  At the end the
-// row groups of a wave merge by shuffles and the waves through LDS; the
+// pass; NS = ceil(C / L) ranges per (sequence, KV head)) and streams it in
+// tiles of U passes.  K and V are staggered so that one register set of each
+// suffices: the next tile's K rows (with its write-mask and mask values) are
+// loaded as soon as the current tile is scored, and its V rows as soon as the
+// current tile is accumulated, so each load has the other half's work to
+// arrive.  Loads are buffer loads at loop-invariant 32-bit offsets plus the
+// tile's offset; rows past the cache read 0, and the prefetch after the last
+// tile uses an out-of-range offset (zeros, no memory traffic), so the loop
+// has no peeled tail.  Each row group (the LPR lanes
+// sharing a row) keeps an online softmax per query head -- running maximum
+// and exp-sum, rescaled once per tile -- and its lanes' slices of P V in
+// registers, so V is never staged in LDS.  A tile without blended rows (the
+// common case in place: only the new token's row has w != 0) takes a path
+// without the blend and the cache stores, chosen once per wave.  At the end
+// the row groups of a wave merge by shuffles and the waves through LDS; the
 // workgroup writes the chunk kernel's partials (or the output, when one
 // range covers the cache) and the same combine follows.  Scores, blended
 // rows and cache writes keep the chunk kernel's rounding; the score divisor
@@ -538,8 +538,6 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
   __shared__ float ks[kHead], vs[kHead];
   __shared__ float wmax[NW][G], wsum[NW][G];
   __shared__ float wacc[NW][G][kHead];
-  __shared__ uint4 stash_k[U][kThreads], stash_v[U][kThreads];
-  __shared__ float stash_w[U][kThreads], stash_m[U][kThreads];
 
   const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
   const int64_t L = a.n[29];
@@ -577,39 +575,31 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
     moff[u] = static_cast<int>((head * mh + r * mc) * S);
   }
 
-  // One tile's rows in registers: K, V, write-mask and mask values.
-  struct Tile {
-    uint4 k[U], v[U];
-    float w[U], m[U];
-  };
+  uint4 kbuf[U], vbuf[U];
+  float wbuf[U], mbuf[U];
   // Tile t's loads; past the last tile every offset is out of range, so
   // the loads return 0 without touching memory.
   constexpr int kPast = 0x7fff0000;
-  auto issue_k = [&](Tile& x, int64_t t) {
+  auto issue_k = [&](int64_t t) {
     const int64_t r0 = c0 + t * TR;
     const bool in = t < ntiles;
     const int tk = in ? static_cast<int>(r0 * kHead * S) : kPast, tw = in ? static_cast<int>(r0 * wc * S) : kPast,
               tm = in ? static_cast<int>(r0 * mc * S) : kPast;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      x.k[u] = buffer_row(krs, koff[u] + tk);
-      x.w[u] = buffer_scalar<T>(wrs, woff[u] + tw);
+      kbuf[u] = buffer_row(krs, koff[u] + tk);
+      wbuf[u] = buffer_scalar<T>(wrs, woff[u] + tw);
       const float mv = buffer_scalar<T>(mrs, moff[u] + tm);
-      x.m[u] = masked ? mv : 0.f;
+      mbuf[u] = masked ? mv : 0.f;
     }
   };
-  auto issue_v = [&](Tile& x, int64_t t) {
+  auto issue_v = [&](int64_t t) {
     const int tk = t < ntiles ? static_cast<int>((c0 + t * TR) * kHead * S) : kPast;
 #pragma unroll
-    for (int u = 0; u < U; ++u) x.v[u] = buffer_row(vrs, koff[u] + tk);
+    for (int u = 0; u < U; ++u) vbuf[u] = buffer_row(vrs, koff[u] + tk);
   };
-  // Two tiles in flight per wave: tile t + 2 is loaded into the register set
-  // that tile t just left.
-  Tile ta, tb;
-  issue_k(ta, 0);
-  issue_v(ta, 0);
-  issue_k(tb, 1);
-  issue_v(tb, 1);
+  issue_k(0);
+  issue_v(0);
 
   // -- RoPE of q and k (the position load, then the table).
   const int32_t* positions = static_cast<const int32_t*>(a.p[3]);
@@ -664,8 +654,13 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
 #pragma unroll
     for (int e = 0; e < V; ++e) acc[h][e] = 0.f;
   }
-  // Blend of a cache row with the new row.
+  // the new token's k' and v slices of this lane, packed in T (exact)
+  const uint4 knew = pack<T>(&ks[part * V]), vnew = pack<T>(&vs[part * V]);
+  // Blend of a cache row with the new row.  The fresh values pass through an
+  // empty asm first, so nothing derived from them is hoisted out of the rare
+  // slow path into registers held across the whole loop.
   auto blend = [&](uint4& row, float w, uint4 fresh) {
+    asm volatile("" : "+v"(fresh.x), "+v"(fresh.y), "+v"(fresh.z), "+v"(fresh.w));
     float x[V], f[V];
     unpack<T>(row, x);
     unpack<T>(fresh, f);
@@ -679,22 +674,43 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
   // the cache row of row j: in place, or the new buffer's contiguous layout
   auto dst_row = [&](int64_t j) { return in_place ? cb + j * kHead : ((b * KV + g) * C + j) * kHead; };
 
-  float s[U][G];
-  // Scores of the tile's U rows for all G heads from the rows as given (the
-  // reduce-scatter leaves each lane one head's dot product; the row group
-  // then shares them) and one rescale of the running state.  The main pass
-  // scores the rows with w == 0 (blended = false), the patch those with
-  // w != 0; the other rows, and rows outside the range, score -inf.
-  auto score = [&](const uint4 (&rows)[U], const Tile& x, int64_t t, bool blended) {
+  float s[U][G], wt[U];
+  // Slow path of a tile (chosen once per wave): the rows with w != 0 are
+  // blended in their register buffers and written to the cache (every row
+  // is written when the cache goes to a new buffer); the shared scoring and
+  // accumulation below then see the blended rows.
+  auto prep_k = [&](int64_t t) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = c0 + t * TR + u * RPP + rgi;
+      const float w = wbuf[u];
+      if (w != 0.f) blend(kbuf[u], w, knew);
+      if (j < c1 && (!in_place || w != 0.f)) reinterpret_cast<uint4*>(Ko + dst_row(j))[part] = kbuf[u];
+    }
+  };
+  auto prep_v = [&](int64_t t) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      const float w = wt[u];
+      if (w != 0.f) blend(vbuf[u], w, vnew);
+      if (j < c1 && (!in_place || w != 0.f)) reinterpret_cast<uint4*>(Vo + dst_row(j))[part] = vbuf[u];
+    }
+  };
+  // Scores of the tile's U rows for all G heads (the reduce-scatter leaves
+  // each lane one head's dot product; the row group then shares them) and
+  // one rescale of the running state.
+  auto score = [&](int64_t t) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
+      wt[u] = wbuf[u];
       float d[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) d[h] = RowDot<T>::dot(rows[u], qp[h]);
+      for (int h = 0; h < G; ++h) d[h] = RowDot<T>::dot(kbuf[u], qp[h]);
       float sc = E::round(E::round(reduce_scatter<G, LPR>(d, part)) * rdiv);
-      sc = E::round(sc + x.m[u]);
-      sc = (j < c1 && (x.w[u] != 0.f) == blended) ? sc : -INFINITY;
+      sc = E::round(sc + mbuf[u]);
+      sc = j < c1 ? sc : -INFINITY;
 #pragma unroll
       for (int h = 0; h < G; ++h) s[u][h] = G == 1 ? sc : __shfl(sc, (lane & ~(LPR - 1)) + h * (LPR / G), 64);
     }
@@ -710,12 +726,13 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
       for (int e = 0; e < V; ++e) acc[h][e] *= f;
     }
   };
-  // exp-sums and P V of the tile's rows (a row scored -inf adds nothing).
-  auto accumulate = [&](const uint4 (&rows)[U]) {
+  // exp-sums and P V of the tile's rows.
+  auto accumulate = [&](int64_t t) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int64_t j = c0 + t * TR + u * RPP + rgi;
       float vf[V];
-      unpack<T>(rows[u], vf);
+      unpack<T>(j < c1 ? vbuf[u] : make_uint4(0, 0, 0, 0), vf);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const float p = s[u][h] == -INFINITY ? 0.f : __expf(s[u][h] - m[h]);
@@ -725,95 +742,22 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
       }
     }
   };
-  // A copied cache takes every row of the range that is not blended, as read.
-  auto copy_rows = [&](const uint4 (&rows)[U], const Tile& x, int64_t t, T* dst) {
+  // blended rows or a copied cache make the tile slow, for the whole wave
+  auto slow_tile = [&]() {
+    bool any = !in_place;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = c0 + t * TR + u * RPP + rgi;
-      if (j < c1 && x.w[u] == 0.f) reinterpret_cast<uint4*>(dst + dst_row(j))[part] = rows[u];
-    }
-  };
-  // Rows with w != 0 (in place: only the new token's row, in one tile of the
-  // cache) are left out of the main pass and handled here, for the whole
-  // wave: blended into temporaries, written to the cache, then scored and
-  // accumulated like the others.  Blending in the tile's own registers would
-  // make the compiler keep a second copy of both register sets.
-  auto patch = [&](const Tile& x, int64_t t) {
-    // the new token's k' and v slices of this lane, packed in T (exact)
-    const uint4 knew = pack<T>(&ks[part * V]), vnew = pack<T>(&vs[part * V]);
-    uint4 kb[U], vb[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = c0 + t * TR + u * RPP + rgi;
-      const float w = x.w[u];
-      kb[u] = x.k[u];
-      vb[u] = x.v[u];
-      if (w != 0.f) {
-        blend(kb[u], w, knew);
-        blend(vb[u], w, vnew);
-        if (j < c1) {
-          reinterpret_cast<uint4*>(Ko + dst_row(j))[part] = kb[u];
-          reinterpret_cast<uint4*>(Vo + dst_row(j))[part] = vb[u];
-        }
-      }
-    }
-    score(kb, x, t, true);
-    accumulate(vb);
-  };
-  // Tile t from register set x, whose next tile is t + 2.  A tile past the
-  // range (the second of the last pair when the count is odd) reads zeros
-  // and scores -inf: it changes nothing.  A tile with rows to blend is only
-  // flagged here (bit t of pending), and the first such tile of the wave is
-  // kept in LDS; patch() runs after the loop, so that no register of the
-  // loop is modified under a branch (which would make the compiler hold a
-  // second copy of both register sets).
-  uint64_t pending = 0;  // wave-uniform
-  int64_t stashed = -1;
-  auto step = [&](Tile& x, int64_t t) {
-    score(x.k, x, t, false);
-    if (!in_place) copy_rows(x.k, x, t, Ko);
-    accumulate(x.v);
-    if (!in_place) copy_rows(x.v, x, t, Vo);
-    bool any = false;
-#pragma unroll
-    for (int u = 0; u < U; ++u) any = any || x.w[u] != 0.f;
-    if (__any(any)) {
-      pending |= uint64_t(1) << t;
-      if (stashed < 0) {
-        stashed = t;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          stash_k[u][tid] = x.k[u];
-          stash_v[u][tid] = x.v[u];
-          stash_w[u][tid] = x.w[u];
-          stash_m[u][tid] = x.m[u];
-        }
-      }
-    }
-    issue_k(x, t + 2);
-    issue_v(x, t + 2);
+    for (int u = 0; u < U; ++u) any = any || wbuf[u] != 0.f;
+    return __any(any) != 0;
   };
 
-  for (int64_t t = 0; t < ntiles; t += 2) {
-    step(ta, t);
-    step(tb, t + 1);
-  }
-  while (pending) {
-    const int64_t t = __builtin_ctzll(pending);
-    pending &= pending - 1;
-    if (t == stashed) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        ta.k[u] = stash_k[u][tid];
-        ta.v[u] = stash_v[u][tid];
-        ta.w[u] = stash_w[u][tid];
-        ta.m[u] = stash_m[u][tid];
-      }
-    } else {
-      issue_k(ta, t);
-      issue_v(ta, t);
-    }
-    patch(ta, t);
+  for (int64_t t = 0; t < ntiles; ++t) {
+    const bool slow = slow_tile();
+    if (slow) prep_k(t);
+    score(t);
+    issue_k(t + 1);
+    if (slow) prep_v(t);
+    accumulate(t);
+    issue_v(t + 1);
   }
 
   // -- merge the row groups of each wave (shuffles), then the waves (LDS).
@@ -1249,7 +1193,6 @@ const char* plan_decode_attn(KArgs& a, Launch& l) {
     if (L <= 0 || L % rpp) return "decode_attn: rows per workgroup must be a positive multiple of the rows per pass";
     if (u != 2 && u != 4) return "decode_attn: passes per tile must be 2 or 4";
     if ((C + L - 1) / L > kMaxChunks) return "decode_attn: more than 64 cache ranges per KV head";
-    if ((L + rpp * u - 1) / (rpp * u) > 64) return "decode_attn: more than 64 tiles per workgroup";
     int e2 = 0;
     if (!(a.f[0] > 0.f) || std::frexp(a.f[0], &e2) != 0.5f)
       return "decode_attn: the streaming kernel needs a power-of-two score divisor";

@@ -24,6 +24,8 @@
 #include "chip.h"
 #include "chomik_hip.h"
 
+#include <cstdlib>
+
 namespace chip {
 namespace {
 
@@ -243,11 +245,18 @@ const char* plan_gemm(KArgs& a, Launch& l) {
     }
     if (total != N) return "gemm: segment widths must add up to N";
   }
-  // 128 x 128 tiles once they fill the chip twice over, else 64 x 64 (output
-  // tiles are half as wide with the SiLU pair)
+  // 128 x 128 tiles once they outnumber the 256 CUs, else 64 x 64 (output
+  // tiles are half as wide with the SiLU pair).  Measured at C3: the q/k/v
+  // GEMM (320 big tiles) 55 -> 45 us with big tiles, the o and down GEMMs
+  // (exactly 256) 39 -> 46 and 100 -> 108 us, so 256 stay small.
+  // CHOMIK_HIP_GEMM_BIG_TILES moves the threshold.
+  static const int64_t big_from = [] {
+    const char* v = std::getenv("CHOMIK_HIP_GEMM_BIG_TILES");
+    return v && *v ? std::atoll(v) : 257;
+  }();
   const int64_t span = silu ? 2 : 1;
   const int64_t big_tiles = ((M + 127) / 128) * ((N * span + 127) / 128);
-  const bool big = big_tiles >= 512;
+  const bool big = big_tiles >= big_from;
   const int64_t bm = big ? 128 : 64, on = bm / span;
   const int64_t tiles = ((M + bm - 1) / bm) * ((N + on - 1) / on);
   const int64_t blocks = 8 * ((tiles + 7) / 8);

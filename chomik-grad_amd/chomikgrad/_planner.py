@@ -601,7 +601,8 @@ class Emitter:
             dense = self.new_value(swapped, node.dtype, "placement")
             strides = dense.strides[:-2] + (dense.strides[-1], dense.strides[-2])
             out = PV(shape, node.dtype, strides, dense.storage, dense.offset)
-            self.add(K_FILL, [], [dense], words=(dense.size * dense.itemsize + 3) // 4)
+            if a.shape[-1] != shape[-1]:  # columns past S: zeros (S == C: the copy covers all)
+                self.add(K_FILL, [], [dense], words=(dense.size * dense.itemsize + 3) // 4)
             view = PV(a.shape, node.dtype, strides, dense.storage, dense.offset)
             self.add(K_COPY, [a], [view])
             return out

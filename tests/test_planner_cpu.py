@@ -197,17 +197,19 @@ def test_prefill_with_cache_placement():
         np.testing.assert_allclose(value, reference, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("cache_length", [16, 12], ids=["cache16", "cache12"])
 @pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
-def test_half_precision_prefill_uses_mfma_gemm(dtype):
+def test_half_precision_prefill_uses_mfma_gemm(dtype, cache_length):
     """Prefill linears of a 16-bit model with more than 8 rows become K_GEMM
     steps (row-major activations times W^T, fp32 accumulation, one rounding):
-    the tape model of those steps matches the oracle's np.matmul."""
+    the tape model of those steps matches the oracle's np.matmul.  A cache
+    as long as the prompt is placed by the copy alone (no zero fill)."""
     config = LlamaConfig(vocab_size=128, hidden_size=256, intermediate_size=688, num_hidden_layers=1,
                          num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64)
     host = synthetic.host_weights(config, dtype, seed=11)
     weights = synthetic.weights_as_tensors(host)
     S = 12
-    model = LlamaForCausalLM(config, weights, sequence_length=S, cache_length=16, dtype=dtype)
+    model = LlamaForCausalLM(config, weights, sequence_length=S, cache_length=cache_length, dtype=dtype)
     ids = np.random.default_rng(4).integers(0, 128, (1, S)).astype(np.int32)
     tokens = Tensor(ids, copy=False)
     outputs = model.prefill(tokens, Tensor(position_selector(S - 1, S, dtype=dtype)))
@@ -219,9 +221,10 @@ def test_half_precision_prefill_uses_mfma_gemm(dtype):
     assert sum(g.attrs.get("up") is not None for g in gemms) == 1
     assert sum(g.attrs.get("res") is not None for g in gemms) == 2
     assert not any(s.kind == K_ELEMENTWISE for s in planned.steps)
-    # the cache placements K^T @ eye(S, C) become fill + strided copy; the one
-    # the last-row selector (a one-hot constant) is a row copy: no generic matmul left
-    assert sum(s.kind == K_FILL for s in planned.steps) == 2
+    # the cache placements K^T @ eye(S, C) become fill + strided copy (the
+    # copy alone when S == C); the last-row selector (a one-hot constant) is
+    # a row copy: no generic matmul left
+    assert sum(s.kind == K_FILL for s in planned.steps) == (2 if cache_length > S else 0)
     assert sum(s.kind == K_MATMUL for s in planned.steps) == 0
     for value, reference in zip(got, expected):
         v, r = np.asarray(value), np.asarray(reference)

@@ -163,14 +163,40 @@ template <> __device__ __forceinline__ uint4 pack<float>(const float* f) {
   return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
 }
 
+// The value of lane (this lane xor o), every lane of the wave active.  Offsets
+// 1, 2, 4 and 8 are DPP lane moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// quad_perm [3,2,1,0] then row_half_mirror, row_ror:8; checked lane by lane
+// on an MI355X), a VALU instruction instead of an LDS-pipe ds_bpermute in
+// the reduction chains; other offsets use __shfl_xor.  With o a constant
+// (unrolled loops) the switch folds away.
+__device__ __forceinline__ int dpp_move(int x, int ctrl) {
+  switch (ctrl) {
+    case 0xB1: return __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false);
+    case 0x4E: return __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false);
+    case 0x1B: return __builtin_amdgcn_update_dpp(x, x, 0x1B, 0xF, 0xF, false);
+    case 0x141: return __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false);
+    default: return __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false);
+  }
+}
+__device__ __forceinline__ float shfl_xor_k(float v, int o) {
+  const int x = __builtin_bit_cast(int, v);
+  switch (o) {
+    case 1: return __builtin_bit_cast(float, dpp_move(x, 0xB1));
+    case 2: return __builtin_bit_cast(float, dpp_move(x, 0x4E));
+    case 4: return __builtin_bit_cast(float, dpp_move(dpp_move(x, 0x1B), 0x141));
+    case 8: return __builtin_bit_cast(float, dpp_move(x, 0x128));
+    default: return __shfl_xor(v, o, 64);
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  for (int off = 32; off > 0; off >>= 1) v += shfl_xor_k(v, off);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, shfl_xor_k(v, off));
   return v;
 }
 

@@ -78,12 +78,12 @@ __device__ __forceinline__ float reduce_scatter(float (&d)[G], int p) {
           // folded into a runtime-indexed access of the whole array (a
           // chain of G selects per element).
           asm volatile("" : "+v"(lo), "+v"(hi));
-          d[i] = (upper ? hi : lo) + __shfl_xor(upper ? lo : hi, o, 64);
+          d[i] = (upper ? hi : lo) + shfl_xor_k(upper ? lo : hi, o);
         }
       }
       held = half;
     } else {
-      d[0] += __shfl_xor(d[0], o, 64);
+      d[0] += shfl_xor_k(d[0], o);
     }
   }
   return d[0];
@@ -157,11 +157,11 @@ __device__ __forceinline__ void combine_chunks(const KArgs& a, int64_t b, int64_
     const float mk = lane < NS ? mk_[x] : -INFINITY;
     float m = mk;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = nan_max(m, __shfl_xor(m, o, 64));
+    for (int o = 32; o > 0; o >>= 1) m = nan_max(m, shfl_xor_k(m, o));
     const float f = lane < NS ? __expf(mk - m) : 0.f;
     float l = lane < NS ? lk_[x] * f : 0.f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    for (int o = 32; o > 0; o >>= 1) l += shfl_xor_k(l, o);
     fac[h][lane] = f / l;
   }
   __syncthreads();
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
   // chunk maximum of this lane's head: across the wave's row groups, then
   // the waves (lanes of row group 0 publish one value per head)
 #pragma unroll
-  for (int o = LPR; o < 64; o <<= 1) mloc = nan_max(mloc, __shfl_xor(mloc, o, 64));
+  for (int o = LPR; o < 64; o <<= 1) mloc = nan_max(mloc, shfl_xor_k(mloc, o));
   if (lane < LPR) red[wave][head] = mloc;
   __syncthreads();
   float m = red[0][head];
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
     for (int e2 = 0; e2 < V; ++e2) vsh[r][part * V + e2] = vf[e2];
   }
 #pragma unroll
-  for (int o = LPR; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o, 64);
+  for (int o = LPR; o < 64; o <<= 1) lsum += shfl_xor_k(lsum, o);
   if (lane < LPR) red2[wave][head] = lsum;
   __syncthreads();  // es, vsh, red, red2 complete
   if (tid < G) {
@@ -765,16 +765,16 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
   for (int h = 0; h < G; ++h) {
     float M = m[h];
 #pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) M = nan_max(M, __shfl_xor(M, o, 64));
+    for (int o = LPR; o < 64; o <<= 1) M = nan_max(M, shfl_xor_k(M, o));
     const float f = M == m[h] ? 1.f : __expf(m[h] - M);
     float ls = l[h] * f;
 #pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) ls += __shfl_xor(ls, o, 64);
+    for (int o = LPR; o < 64; o <<= 1) ls += shfl_xor_k(ls, o);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       float x = acc[h][e] * f;
 #pragma unroll
-      for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
+      for (int o = LPR; o < 64; o <<= 1) x += shfl_xor_k(x, o);
       acc[h][e] = x;
     }
     if (lane < LPR) {

@@ -1203,11 +1203,11 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_attn_proj(KArgs a) {
     const float mk = lane < NS ? mk_[x] : -INFINITY;
     float m = mk;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = proj_nan_max(m, __shfl_xor(m, o, 64));
+    for (int o = 32; o > 0; o >>= 1) m = proj_nan_max(m, shfl_xor_k(m, o));
     const float f = lane < NS ? __expf(mk - m) : 0.f;
     float l = lane < NS ? lk_[x] * f : 0.f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    for (int o = 32; o > 0; o >>= 1) l += shfl_xor_k(l, o);
     if (lane < kProjChunks) fac[h][lane] = f / l;
   }
   __syncthreads();

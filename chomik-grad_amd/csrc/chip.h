@@ -165,10 +165,12 @@ template <> __device__ __forceinline__ uint4 pack<float>(const float* f) {
 
 // The value of lane (this lane xor o), every lane of the wave active.  Offsets
 // 1, 2, 4 and 8 are DPP lane moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
-// quad_perm [3,2,1,0] then row_half_mirror, row_ror:8; checked lane by lane
-// on an MI355X), a VALU instruction instead of an LDS-pipe ds_bpermute in
-// the reduction chains; other offsets use __shfl_xor.  With o a constant
-// (unrolled loops) the switch folds away.
+// quad_perm [3,2,1,0] then row_half_mirror, row_ror:8), 16 and 32 gfx950's
+// v_permlane16_swap / v_permlane32_swap of the value with itself (the first
+// result holds the lower row / half in both, the second the upper) and a
+// select on the lane's bit; all checked lane by lane on an MI355X.  They are
+// VALU instructions instead of an LDS-pipe ds_bpermute in the reduction
+// chains.  With o a constant (unrolled loops) the switch folds away.
 __device__ __forceinline__ int dpp_move(int x, int ctrl) {
   switch (ctrl) {
     case 0xB1: return __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false);
@@ -185,6 +187,14 @@ __device__ __forceinline__ float shfl_xor_k(float v, int o) {
     case 2: return __builtin_bit_cast(float, dpp_move(x, 0x4E));
     case 4: return __builtin_bit_cast(float, dpp_move(dpp_move(x, 0x1B), 0x141));
     case 8: return __builtin_bit_cast(float, dpp_move(x, 0x128));
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+      return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+    }
+    case 32: {
+      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+      return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+    }
     default: return __shfl_xor(v, o, 64);
   }
 }

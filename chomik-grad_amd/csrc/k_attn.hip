@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
     const float s = load_f(a.p[4], pos * kHead + 32 + i, dt);
     // lane d < 32 holds x[d] (partner x[d + 32]); lane d >= 32 holds x[d]
     auto rope = [&](float x) {
-      const float p = __shfl_xor(x, 32, 64);
+      const float p = shfl_xor_k(x, 32);
       return E::round(lane < 32 ? __fadd_rn(__fmul_rn(x, c), __fmul_rn(p, -s))
                                 : __fadd_rn(__fmul_rn(p, s), __fmul_rn(x, c)));
     };
@@ -624,7 +624,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
     const float c = load_f(a.p[4], pos * kHead + i, dt);
     const float sn = load_f(a.p[4], pos * kHead + 32 + i, dt);
     auto rope = [&](float x) {
-      const float p = __shfl_xor(x, 32, 64);
+      const float p = shfl_xor_k(x, 32);
       return E::round(lane < 32 ? __fadd_rn(__fmul_rn(x, c), __fmul_rn(p, -sn))
                                 : __fadd_rn(__fmul_rn(p, sn), __fmul_rn(x, c)));
     };
@@ -1029,8 +1029,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void k_decode_attn_mfma(KArgs a) {
       }
     }
   }
-  mx = nan_max(mx, __shfl_xor(mx, 16, 64));
-  mx = nan_max(mx, __shfl_xor(mx, 32, 64));
+  mx = nan_max(mx, shfl_xor_k(mx, 16));
+  mx = nan_max(mx, shfl_xor_k(mx, 32));
 
   // -- P (rounded to the cache dtype; the exp-sum adds the rounded values)
   // and P V through the wave's LDS tile
@@ -1065,8 +1065,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void k_decode_attn_mfma(KArgs a) {
       }
     }
   }
-  ls += __shfl_xor(ls, 16, 64);
-  ls += __shfl_xor(ls, 32, 64);
+  ls += shfl_xor_k(ls, 16);
+  ls += shfl_xor_k(ls, 32);
 
   // -- merge the waves: O (lane: heads 4 grp + r, dim 16 db + col), maxima
   // and exp-sums per head

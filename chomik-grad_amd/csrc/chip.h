@@ -170,44 +170,106 @@ template <> __device__ __forceinline__ uint4 pack<float>(const float* f) {
 // result holds the lower row / half in both, the second the upper) and a
 // select on the lane's bit; all checked lane by lane on an MI355X.  They are
 // VALU instructions instead of an LDS-pipe ds_bpermute in the reduction
-// chains.  With o a constant (unrolled loops) the switch folds away.
+// chains.  With o a constant (unrolled loops) the switch folds away.  Every
+// lane of a row has a source under these controls, so bound_ctrl changes no
+// value; with it set (and no old value) the compiler folds a move into the
+// VALU instruction that consumes it (v_add_f32_dpp).
 __device__ __forceinline__ int dpp_move(int x, int ctrl) {
   switch (ctrl) {
-    case 0xB1: return __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false);
-    case 0x4E: return __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false);
-    case 0x1B: return __builtin_amdgcn_update_dpp(x, x, 0x1B, 0xF, 0xF, false);
-    case 0x141: return __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false);
-    default: return __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false);
+    case 0xB1: return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);
+    case 0x4E: return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);
+    case 0x1B: return __builtin_amdgcn_mov_dpp(x, 0x1B, 0xF, 0xF, true);
+    case 0x141: return __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true);
+    default: return __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);
   }
 }
-__device__ __forceinline__ float shfl_xor_k(float v, int o) {
-  const int x = __builtin_bit_cast(int, v);
-  switch (o) {
-    case 1: return __builtin_bit_cast(float, dpp_move(x, 0xB1));
-    case 2: return __builtin_bit_cast(float, dpp_move(x, 0x4E));
-    case 4: return __builtin_bit_cast(float, dpp_move(dpp_move(x, 0x1B), 0x141));
-    case 8: return __builtin_bit_cast(float, dpp_move(x, 0x128));
-    case 16: {
-      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-      return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
-    }
-    case 32: {
-      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-      return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
-    }
-    default: return __shfl_xor(v, o, 64);
+// Both registers a permlane swap writes.  The elements are read into ints
+// before any bit cast: a __builtin_bit_cast of an element of the returned
+// vector is compiled as a read of element 0.
+struct LanePair {
+  int first, second;
+};
+template <int O>
+__device__ __forceinline__ LanePair permlane_swap(int x, int y) {
+  static_assert(O == 16 || O == 32, "permlane swaps exchange rows (16) or halves (32)");
+  if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+    const int a = r[0], b = r[1];
+    return {a, b};
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    const int a = r[0], b = r[1];
+    return {a, b};
   }
+}
+// The offset is a template argument so that every exchange is resolved at
+// compile time: with a runtime offset the compiler keeps the convergent lane
+// moves behind run-time branches instead of unrolling the reduction loops.
+template <int O>
+__device__ __forceinline__ float shfl_xor_k(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  if constexpr (O == 1) return __builtin_bit_cast(float, dpp_move(x, 0xB1));
+  else if constexpr (O == 2) return __builtin_bit_cast(float, dpp_move(x, 0x4E));
+  else if constexpr (O == 4) return __builtin_bit_cast(float, dpp_move(dpp_move(x, 0x1B), 0x141));
+  else if constexpr (O == 8) return __builtin_bit_cast(float, dpp_move(x, 0x128));
+  else {
+    const LanePair r = permlane_swap<O>(x, x);
+    return __builtin_bit_cast(float, (threadIdx.x & O) ? r.first : r.second);
+  }
+}
+// v + v(lane xor O): the same value as v + shfl_xor_k<O>(v) (IEEE addition
+// commutes).  At 16 and 32 the swap of v with itself leaves this lane's value
+// in one register and the partner's in the other, so no select is needed.
+template <int O>
+__device__ __forceinline__ float add_xor(float v) {
+  if constexpr (O == 16 || O == 32) {
+    const int x = __builtin_bit_cast(int, v);
+    const LanePair r = permlane_swap<O>(x, x);
+    return __builtin_bit_cast(float, r.first) + __builtin_bit_cast(float, r.second);
+  } else {
+    return v + shfl_xor_k<O>(v);
+  }
+}
+// One butterfly step of a reduce-scatter: lanes whose bit O is clear
+// (upper false) return lo + lo(lane xor O), lanes whose bit is set hi +
+// hi(lane xor O).  upper must be the lane's bit O.  At 16 and 32 one swap of
+// lo with hi moves exactly those operands into its two registers: the first
+// holds this lane's lo (bit clear) or the partner's hi (bit set), the second
+// the partner's lo or this lane's hi.
+template <int O>
+__device__ __forceinline__ float add_xor_halves(float lo, float hi, bool upper) {
+  if constexpr (O == 16 || O == 32) {
+    const LanePair r = permlane_swap<O>(__builtin_bit_cast(int, lo), __builtin_bit_cast(int, hi));
+    return __builtin_bit_cast(float, r.first) + __builtin_bit_cast(float, r.second);
+  } else {
+    return (upper ? hi : lo) + shfl_xor_k<O>(upper ? lo : hi);
+  }
+}
+// Butterfly sum over lane offsets O, then O*2 up to LAST (O < LAST) or O/2
+// down to LAST (O > LAST); offsets of 64 and above are no step.
+template <int O, int LAST>
+__device__ __forceinline__ float sum_xor(float v) {
+  if constexpr (O >= 1 && O < 64) {
+    v = add_xor<O>(v);
+    if constexpr (O < LAST) return sum_xor<O * 2, LAST>(v);
+    else if constexpr (O > LAST) return sum_xor<O / 2, LAST>(v);
+  }
+  return v;
+}
+// The same walk with v = op(v, partner's v).
+template <int O, int LAST, class Op>
+__device__ __forceinline__ float reduce_xor(float v, Op op) {
+  if constexpr (O >= 1 && O < 64) {
+    v = op(v, shfl_xor_k<O>(v));
+    if constexpr (O < LAST) return reduce_xor<O * 2, LAST>(v, op);
+    else if constexpr (O > LAST) return reduce_xor<O / 2, LAST>(v, op);
+  }
+  return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += shfl_xor_k(v, off);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return sum_xor<32, 1>(v); }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, shfl_xor_k(v, off));
-  return v;
+  return reduce_xor<32, 1>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Values exchanged between workgroups that may sit on different XCDs (each

@@ -62,30 +62,31 @@ __device__ __forceinline__ int scatter_head(int p) {
   }
   return head;
 }
-template <int G, int L>
-__device__ __forceinline__ float reduce_scatter(float (&d)[G], int p) {
-  int held = G;
+template <int G, int O, int HELD>
+__device__ __forceinline__ void reduce_scatter_steps(float (&d)[G], int p) {
+  if constexpr (O >= 1) {
+    if constexpr (HELD > 1) {
+      constexpr int half = HELD / 2;
+      const bool upper = (p & O) != 0;
 #pragma unroll
-  for (int o = L / 2; o >= 1; o >>= 1) {
-    if (held > 1) {
-      const int half = held >> 1;
-      const bool upper = (p & o) != 0;
-#pragma unroll
-      for (int i = 0; i < G / 2; ++i) {
-        if (i < half) {
-          float lo = d[i], hi = d[i + half];
-          // Opaque copies: a select between two elements of d would be
-          // folded into a runtime-indexed access of the whole array (a
-          // chain of G selects per element).
-          asm volatile("" : "+v"(lo), "+v"(hi));
-          d[i] = (upper ? hi : lo) + shfl_xor_k(upper ? lo : hi, o);
-        }
+      for (int i = 0; i < half; ++i) {
+        float lo = d[i], hi = d[i + half];
+        // Opaque copies: a select between two elements of d would be
+        // folded into a runtime-indexed access of the whole array (a
+        // chain of G selects per element).
+        asm volatile("" : "+v"(lo), "+v"(hi));
+        d[i] = add_xor_halves<O>(lo, hi, upper);
       }
-      held = half;
+      reduce_scatter_steps<G, O / 2, half>(d, p);
     } else {
-      d[0] += shfl_xor_k(d[0], o);
+      d[0] = add_xor<O>(d[0]);
+      reduce_scatter_steps<G, O / 2, 1>(d, p);
     }
   }
+}
+template <int G, int L>
+__device__ __forceinline__ float reduce_scatter(float (&d)[G], int p) {
+  reduce_scatter_steps<G, L / 2, G>(d, p);
   return d[0];
 }
 
@@ -156,12 +157,10 @@ __device__ __forceinline__ void combine_chunks(const KArgs& a, int64_t b, int64_
     if (h >= G) break;
     const float mk = lane < NS ? mk_[x] : -INFINITY;
     float m = mk;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = nan_max(m, shfl_xor_k(m, o));
+    m = reduce_xor<32, 1>(m, [](float a, float b) { return nan_max(a, b); });
     const float f = lane < NS ? __expf(mk - m) : 0.f;
     float l = lane < NS ? lk_[x] * f : 0.f;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += shfl_xor_k(l, o);
+    l = sum_xor<32, 1>(l);
     fac[h][lane] = f / l;
   }
   __syncthreads();
@@ -270,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
     const float s = load_f(a.p[4], pos * kHead + 32 + i, dt);
     // lane d < 32 holds x[d] (partner x[d + 32]); lane d >= 32 holds x[d]
     auto rope = [&](float x) {
-      const float p = shfl_xor_k(x, 32);
+      const float p = shfl_xor_k<32>(x);
       return E::round(lane < 32 ? __fadd_rn(__fmul_rn(x, c), __fmul_rn(p, -s))
                                 : __fadd_rn(__fmul_rn(p, s), __fmul_rn(x, c)));
     };
@@ -336,8 +335,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
   }
   // chunk maximum of this lane's head: across the wave's row groups, then
   // the waves (lanes of row group 0 publish one value per head)
-#pragma unroll
-  for (int o = LPR; o < 64; o <<= 1) mloc = nan_max(mloc, shfl_xor_k(mloc, o));
+  mloc = reduce_xor<LPR, 32>(mloc, [](float a, float b) { return nan_max(a, b); });
   if (lane < LPR) red[wave][head] = mloc;
   __syncthreads();
   float m = red[0][head];
@@ -364,8 +362,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
 #pragma unroll
     for (int e2 = 0; e2 < V; ++e2) vsh[r][part * V + e2] = vf[e2];
   }
-#pragma unroll
-  for (int o = LPR; o < 64; o <<= 1) lsum += shfl_xor_k(lsum, o);
+  lsum = sum_xor<LPR, 32>(lsum);
   if (lane < LPR) red2[wave][head] = lsum;
   __syncthreads();  // es, vsh, red, red2 complete
   if (tid < G) {
@@ -624,7 +621,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
     const float c = load_f(a.p[4], pos * kHead + i, dt);
     const float sn = load_f(a.p[4], pos * kHead + 32 + i, dt);
     auto rope = [&](float x) {
-      const float p = shfl_xor_k(x, 32);
+      const float p = shfl_xor_k<32>(x);
       return E::round(lane < 32 ? __fadd_rn(__fmul_rn(x, c), __fmul_rn(p, -sn))
                                 : __fadd_rn(__fmul_rn(p, sn), __fmul_rn(x, c)));
     };
@@ -764,17 +761,14 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     float M = m[h];
-#pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) M = nan_max(M, shfl_xor_k(M, o));
+    M = reduce_xor<LPR, 32>(M, [](float a, float b) { return nan_max(a, b); });
     const float f = M == m[h] ? 1.f : __expf(m[h] - M);
     float ls = l[h] * f;
-#pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) ls += shfl_xor_k(ls, o);
+    ls = sum_xor<LPR, 32>(ls);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       float x = acc[h][e] * f;
-#pragma unroll
-      for (int o = LPR; o < 64; o <<= 1) x += shfl_xor_k(x, o);
+      x = sum_xor<LPR, 32>(x);
       acc[h][e] = x;
     }
     if (lane < LPR) {
@@ -1029,8 +1023,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void k_decode_attn_mfma(KArgs a) {
       }
     }
   }
-  mx = nan_max(mx, shfl_xor_k(mx, 16));
-  mx = nan_max(mx, shfl_xor_k(mx, 32));
+  mx = nan_max(mx, shfl_xor_k<16>(mx));
+  mx = nan_max(mx, shfl_xor_k<32>(mx));
 
   // -- P (rounded to the cache dtype; the exp-sum adds the rounded values)
   // and P V through the wave's LDS tile
@@ -1065,8 +1059,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void k_decode_attn_mfma(KArgs a) {
       }
     }
   }
-  ls += shfl_xor_k(ls, 16);
-  ls += shfl_xor_k(ls, 32);
+  ls = add_xor<16>(ls);
+  ls = add_xor<32>(ls);
 
   // -- merge the waves: O (lane: heads 4 grp + r, dim 16 db + col), maxima
   // and exp-sums per head

@@ -171,8 +171,8 @@ void k_flash_prefill(KArgs a) {
           tmax = fmaxf(tmax, x[t][r]);
         }
     }
-    tmax = fmaxf(tmax, shfl_xor_k(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_k(tmax, 32));
+    tmax = fmaxf(tmax, shfl_xor_k<16>(tmax));
+    tmax = fmaxf(tmax, shfl_xor_k<32>(tmax));
     const float mnew = fmaxf(m, tmax);
     // every query has an unmasked key in its first tile, so mnew is finite
     // from the first tile on (a -inf - -inf would need an all-masked row)
@@ -239,8 +239,8 @@ void k_flash_prefill(KArgs a) {
     compute(j0 + kBK);
   }
   // row sums: this lane's keys, then the other three key groups of its query
-  lsum += shfl_xor_k(lsum, 16);
-  lsum += shfl_xor_k(lsum, 32);
+  lsum = add_xor<16>(lsum);
+  lsum = add_xor<32>(lsum);
 
   T* out = static_cast<T*>(a.p[4]) + b * a.n[26] + h * a.n[27];
   const int64_t ot = a.n[28];

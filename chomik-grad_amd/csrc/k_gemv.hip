@@ -1202,12 +1202,10 @@ __global__ __launch_bounds__(64 * kProjWaves) void k_attn_proj(KArgs a) {
     if (h >= H) break;
     const float mk = lane < NS ? mk_[x] : -INFINITY;
     float m = mk;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = proj_nan_max(m, shfl_xor_k(m, o));
+    m = reduce_xor<32, 1>(m, [](float a, float b) { return proj_nan_max(a, b); });
     const float f = lane < NS ? __expf(mk - m) : 0.f;
     float l = lane < NS ? lk_[x] * f : 0.f;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += shfl_xor_k(l, o);
+    l = sum_xor<32, 1>(l);
     if (lane < kProjChunks) fac[h][lane] = f / l;
   }
   __syncthreads();

@@ -71,9 +71,11 @@ DECODE_ATTN_MAX_CHUNKS = 64
 # The streaming kernel takes over when the chunk kernel would need more than
 # this many workgroups (several latency-bound rounds); it launches about
 # DECODE_ATTN_STREAM_WGS workgroups with DECODE_ATTN_STREAM_UNROLL passes
-# per tile (2 or 4; 2 measured faster at batch 8 over 4096 cached rows).
+# per tile (2 or 4; 2 measured faster at batch 8 over 4096 cached rows).  At
+# batch 8 x 8 KV heads over 4096 rows, 512 workgroups (two per CU, 512 rows
+# each) measured 0.8 % faster than 768 or 640, and 384 or 256 slower.
 DECODE_ATTN_STREAM_ABOVE = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_ABOVE", "768"))
-DECODE_ATTN_STREAM_WGS = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_WGS", "768"))
+DECODE_ATTN_STREAM_WGS = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_WGS", "512"))
 DECODE_ATTN_STREAM_UNROLL = int(os.environ.get("CHOMIK_HIP_ATTN_STREAM_UNROLL", "2"))
 # Batch-1 decode, opt-in: the chunk attention stores only its partials and
 # the output projection (the next GEMV) combines them instead of the

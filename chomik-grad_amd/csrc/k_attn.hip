@@ -765,18 +765,46 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn_stream(KArgs a) {
     const float f = M == m[h] ? 1.f : __expf(m[h] - M);
     float ls = l[h] * f;
     ls = sum_xor<LPR, 32>(ls);
+    if constexpr (LPR == 8 && V == 8) {
+      // Reduce-scatter over the wave's 8 row groups: each butterfly step
+      // keeps half of the values (the upper half where the lane's bit is
+      // set), so a lane of row group r ends with one element of its part,
+      // element 4 r0 + 2 r1 + r2 (r0..r2 = the bits 8, 16, 32 of the lane).
+      // Every element's sum is the same butterfly as the all-reduce's.
+      const bool u8 = (lane & 8) != 0, u16 = (lane & 16) != 0, u32 = (lane & 32) != 0;
+      float y[4], z[2];
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      float x = acc[h][e] * f;
-      x = sum_xor<LPR, 32>(x);
-      acc[h][e] = x;
-    }
-    if (lane < LPR) {
+      for (int i = 0; i < 4; ++i) {
+        float lo = acc[h][i] * f, hi = acc[h][i + 4] * f;
+        asm volatile("" : "+v"(lo), "+v"(hi));
+        y[i] = add_xor_halves<8>(lo, hi, u8);
+      }
 #pragma unroll
-      for (int e = 0; e < V; ++e) wacc[wave][h][part * V + e] = acc[h][e];
-      if (part == 0) {
+      for (int i = 0; i < 2; ++i) {
+        float lo = y[i], hi = y[i + 2];
+        asm volatile("" : "+v"(lo), "+v"(hi));
+        z[i] = add_xor_halves<16>(lo, hi, u16);
+      }
+      const float sum = add_xor_halves<32>(z[0], z[1], u32);
+      wacc[wave][h][part * V + (u8 ? 4 : 0) + (u16 ? 2 : 0) + (u32 ? 1 : 0)] = sum;
+      if (lane == 0) {
         wmax[wave][h] = M;
         wsum[wave][h] = ls;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float x = acc[h][e] * f;
+        x = sum_xor<LPR, 32>(x);
+        acc[h][e] = x;
+      }
+      if (lane < LPR) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) wacc[wave][h][part * V + e] = acc[h][e];
+        if (part == 0) {
+          wmax[wave][h] = M;
+          wsum[wave][h] = ls;
+        }
       }
     }
   }

@@ -11,7 +11,7 @@ from .generation import (
     verify_greedy_block_with_bonus,
     verify_greedy_candidates,
 )
-from .hip_backend import HIPArray, HIPCompiler, HIPDeviceAdapter, HIPProgram
+from .hip_backend import HIPArray, HIPCompiler, HIPDeviceAdapter, HIPProgram, register_into
 from .lazy import (
     CompiledProgram,
     Compiler,
@@ -60,6 +60,7 @@ __all__ = [
     "no_grad",
     "realize",
     "realize_nodes",
+    "register_into",
     "register_compiler",
     "set_default_compiler",
     "topological_sort",

@@ -34,7 +34,7 @@ from typing import Dict, List, Optional, Sequence, Set, Tuple
 import numpy as np
 
 from .dtypes import BFLOAT16, dtype_code, dtype_name, is_float, is_integer
-from .lazy import GraphPlan, LazyNode, Op
+from .lazy import GraphPlan, LazyNode, Op, op_of
 
 # Step kinds (enum chip_kind in include/chomik_hip.h).
 K_FILL, K_COPY, K_ELEMENTWISE, K_REDUCE, K_GATHER, K_MATMUL, K_SOFTMAX = 1, 2, 3, 4, 5, 6, 7
@@ -218,7 +218,7 @@ class _HipGraphPlan(GraphPlan):
 
 
 def _is_ew(node: LazyNode, kind: str) -> bool:
-    return node.op is Op.ELEMENTWISE and node.arg == kind
+    return op_of(node) is Op.ELEMENTWISE and node.arg == kind
 
 
 def _is_one(node: LazyNode, dynamic: Set[LazyNode]) -> bool:
@@ -235,10 +235,10 @@ def _is_one(node: LazyNode, dynamic: Set[LazyNode]) -> bool:
 
 
 def _match_linear(node: LazyNode):
-    if node.op is not Op.MATMUL:
+    if op_of(node) is not Op.MATMUL:
         return None
     a, b = node.inputs
-    if b.op is Op.PERMUTE and b.arg == (1, 0) and len(b.inputs[0].shape) == 2:
+    if op_of(b) is Op.PERMUTE and b.arg == (1, 0) and len(b.inputs[0].shape) == 2:
         return a, b.inputs[0]
     return None
 
@@ -263,10 +263,10 @@ def _match_kv_update(node: LazyNode, dynamic):
         return None
     if _is_ew(added, "mul") and added.inputs[1] is w:
         return ("kv_write", cache, added.inputs[0], w)
-    if (added.op is Op.PERMUTE and added.arg == (0, 1, 3, 2)
-            and added.inputs[0].op is Op.MATMUL):
+    if (op_of(added) is Op.PERMUTE and added.arg == (0, 1, 3, 2)
+            and op_of(added.inputs[0]) is Op.MATMUL):
         inner, placement = added.inputs[0].inputs
-        if (inner.op is Op.PERMUTE and inner.arg == (0, 1, 3, 2)
+        if (op_of(inner) is Op.PERMUTE and inner.arg == (0, 1, 3, 2)
                 and len(placement.shape) == 2):
             return ("kv_place", cache, inner.inputs[0], placement, w)
     return None
@@ -462,7 +462,7 @@ class Emitter:
     def run(self) -> None:
         nodes = self.plan.nodes()
         for node in nodes:
-            if node.op is not None and node.op is not Op.GATHER:
+            if node.op is not None and op_of(node) is not Op.GATHER:
                 if node.dtype == np.float64:
                     raise TypeError(
                         "the hip backend does not support float64; create this tensor as float32"
@@ -500,7 +500,7 @@ class Emitter:
             handler = getattr(self, "lower_" + kind)
             return handler(node, args, argument)
         args = [self.values[parent] for parent in node.inputs]
-        handler = getattr(self, "op_" + node.op.name.lower())
+        handler = getattr(self, "op_" + op_of(node).name.lower())
         return handler(node, args)
 
     def emit_leaf(self, node: LazyNode) -> PV:
@@ -793,25 +793,35 @@ class Emitter:
     @staticmethod
     def _causal_mask_value(mask: Optional[PV], T: int, C: int, dtype) -> Optional[float]:
         """The value above the diagonal if ``mask`` is a captured constant
-        holding exactly the causal triangle (0 on and below the diagonal, one
-        value <= -1e4 above it) for T == C, else None."""
+        whose every (T, C) slice, read through the view's shape, strides and
+        offset, is exactly the causal triangle (0 on and below the diagonal,
+        one value <= -1e4 above it) for T == C, else None.  Reading through
+        the view matters: a transposed triangle (anti-causal) is a view of
+        the same storage with other strides."""
         if mask is None or T != C or T < 2 or mask.storage.kind != "const":
             return None
         leaf = getattr(mask.storage, "leaf", None)
-        if leaf is None or leaf.value is None or mask.offset or np.dtype(mask.dtype) != np.dtype(dtype):
+        if leaf is None or leaf.value is None or np.dtype(mask.dtype) != np.dtype(dtype):
             return None
-        value = np.asarray(leaf.value)
-        if value.size != T * C:
+        if len(mask.shape) < 2 or tuple(mask.shape[-2:]) != (T, C):
             return None
-        grid = value.reshape(T, C)
-        if grid.dtype == BFLOAT16:
+        flat = np.asarray(leaf.value).reshape(-1)
+        index = mask.offset + sum(
+            np.arange(size).reshape((1,) * axis + (size,) + (1,) * (len(mask.shape) - axis - 1)) * stride
+            for axis, (size, stride) in enumerate(zip(mask.shape, mask.strides)))
+        index = np.broadcast_to(index, mask.shape)
+        if index.size == 0 or index.min() < 0 or index.max() >= flat.size:
+            return None
+        grids = flat[index].reshape(-1, T, C)
+        if grids.dtype == BFLOAT16:
             from .dtypes import bf16_to_float32
-            grid = bf16_to_float32(grid)
-        grid = grid.astype(np.float32)
-        above = grid[np.triu_indices(T, 1)]
-        if not np.all(np.tril(grid) == 0) or above.size == 0 or not np.all(above == above[0]):
+            grids = bf16_to_float32(grids)
+        grids = grids.astype(np.float32)
+        above = grids[:, np.triu_indices(T, 1)[0], np.triu_indices(T, 1)[1]]
+        lower = np.tril(np.ones((T, C), bool))
+        if not np.all(grids[:, lower] == 0) or above.size == 0 or not np.all(above == above.flat[0]):
             return None
-        return float(above[0]) if above[0] <= -1e4 + 16 else None
+        return float(above.flat[0]) if above.flat[0] <= -1e4 + 16 else None
 
     def lower_softmax(self, node, args, axis):
         source = args[0]

@@ -506,3 +506,23 @@ class HIPCompiler(Compiler):
         program = HIPProgram(self, planned, handle.handle, inputs, leaf_map)
         program._handle_owner = handle
         return program
+
+
+def register_into(lazy_module, *, replace: bool = False) -> None:
+    """Register the ``hip`` plugin into another copy of the plugin API.
+
+    ``lazy_module`` is a module with the reference's registry and plugin
+    ABCs (``register_compiler``, ``Compiler``, ``CompiledProgram``,
+    ``DeviceAdapter``; chomikgrad/lazy.py:107-209, 646-678), such as the
+    reference package's own ``chomikgrad.lazy``.  Its ``get_compiler`` checks
+    ``isinstance(compiler, Compiler)`` against its own ABC, so the plugin's
+    classes are registered there as virtual subclasses.  Graphs built from
+    that module's ``LazyNode`` and ``Op`` are planned by operation value
+    (``lazy.op_of``); natives are stored under ``native_values["hip"]``, the
+    name registered here, so that module's ``LazyNode.numpy_value`` reads
+    them back through this plugin's adapter.
+    """
+    lazy_module.Compiler.register(HIPCompiler)
+    lazy_module.CompiledProgram.register(HIPProgram)
+    lazy_module.DeviceAdapter.register(HIPDeviceAdapter)
+    lazy_module.register_compiler("hip", HIPCompiler, replace=replace)

@@ -52,6 +52,20 @@ class Op(Enum):
     GATHER = "gather"
 
 
+def op_of(node: "LazyNode") -> Optional[Op]:
+    """The node's operation as this module's ``Op``, or None for a leaf.
+
+    Nodes built by another copy of the IR (for example the reference
+    package's own ``chomikgrad.lazy``, whose ``Op`` has the same member
+    names and values but is a different class) are matched by value, so a
+    plugin registered into that package's registry plans its graphs too.
+    """
+    op = node.op
+    if op is None or type(op) is Op:
+        return op
+    return Op(op.value)
+
+
 class LazyNode:
     """One value of a lazy graph.
 
@@ -356,7 +370,7 @@ class GraphPlan:
 
         def eligible(node: LazyNode) -> bool:
             return (
-                node.op is Op.ELEMENTWISE
+                op_of(node) is Op.ELEMENTWISE
                 and self.lowering(node) is None
                 and _float_dtype(node.dtype)
             )

@@ -93,6 +93,24 @@ __device__ __forceinline__ float reduce_scatter(float (&d)[G], int p) {
 // The partials are exchanged between workgroups that may sit on different
 // XCDs through store_agent / load_agent; the writer waits for its stores to
 // complete before it takes a ticket.
+//
+// Ordering rests on gfx950 hardware behaviour, not on the HIP/C++ memory
+// model: the ticket is a relaxed agent-scope RMW, so the model gives no
+// happens-before from the writers' partial stores to the last arriver's
+// loads.  What makes it hold on this chip:
+//  - store_agent / load_agent are agent-scope atomics, which compile to
+//    global_store / global_load with sc1: stores write through the XCD's L2
+//    to the memory side, loads miss the L2 and read the memory side, so no
+//    XCD's L2 can hold a stale copy of a partial;
+//  - s_waitcnt(0) waits until every store of the thread is acknowledged,
+//    which the memory side does once the write is visible to every later
+//    sc1 load; the block barrier then covers the other threads' stores;
+//  - the ticket RMW is issued only after that, and the last arriver issues
+//    its partial loads only after it has the ticket's returned value.
+// A release RMW / acquire load pair would make it hold by the model, but at
+// agent scope it compiles to buffer_wbl2 sc1 / buffer_inv sc1 (a writeback
+// and an invalidate of the whole L2) in every workgroup, measured at about
+// 5 us per launch: more than half of the kernel.
 
 // Called by every workgroup of (sequence b, KV head g) after it stored its
 // partials (P V sums, maximum and exp-sum per query head of the group): the

@@ -1058,7 +1058,10 @@ __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) 
   // ticket per tile in the first n[25] bytes, then the partials); the last
   // block of the tile to arrive -- a self-resetting ticket, no spinning --
   // adds the KB partials in block order (the same sum whatever the arrival
-  // order) and finishes.
+  // order) and finishes.  The hand-off is the decode attention's
+  // (k_attn.hip, combine_chunks): sc1 stores and loads that bypass the
+  // XCDs' L2s, the stores acknowledged before the relaxed ticket is taken;
+  // it rests on that gfx950 behaviour, not on release/acquire ordering.
   if (KB > 1) {
     if (a.p[14] == nullptr) {  // a workspace is required (planned with it)
       if (lane == 0) raise_error(a, ERR_SHAPE);

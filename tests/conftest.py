@@ -44,3 +44,16 @@ def tiny_weights(config, seed, dtype=np.float32, scale=0.05):
                               else rng.normal(0, scale, shape).astype(np.float32), dtype))
         for name, shape in required_weight_shapes(config).items()
     }
+
+
+@pytest.fixture(scope="session")
+def tinyllama_runtime(hip):
+    """The C2/C3 model (TinyLlama-1.1B shape, float16 weights from seed 0) on
+    the hip plugin, built once per session: generating its 1.1e9 weights on
+    the host takes about 20 seconds."""
+    from chomikgrad import synthetic
+    from chomikgrad.runtime import LlamaRuntime
+
+    spec = synthetic.TINYLLAMA
+    host = synthetic.host_weights(spec.config, spec.dtype, seed=0)
+    return LlamaRuntime(spec.config, synthetic.weights_as_tensors(host), compiler="hip", dtype=spec.dtype)

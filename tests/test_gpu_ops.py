@@ -322,3 +322,40 @@ def test_prefill_gemm_epilogues_match_oracle(hip, dtype, S):
     expected = realize(*outputs, compiler="cpu")
     for value, reference in zip(got, expected):
         np.testing.assert_allclose(as_float(value), as_float(reference), rtol=2e-2, atol=3e-2)
+
+
+def test_safetensors_bf16_stored_tensor_on_device(hip, tmp_path):
+    """A BF16-stored tensor uploaded as bfloat16 (bits unchanged) and as
+    float32 (exact widening), read back through the adapter."""
+    announce("safetensors BF16-stored tensor")
+    from test_host_cpu import BF16_BITS, BF16_VALUES, write_safetensors
+
+    path = tmp_path / "bf.safetensors"
+    write_safetensors(path, {"w": ("BF16", (8,), BF16_BITS.tobytes())})
+    native = hip.device.load_safetensors(path)
+    assert hip.device.dtype(native["w"]) == BFLOAT16
+    np.testing.assert_array_equal(hip.device.to_numpy(native["w"]).view(np.uint16), BF16_BITS)
+    wide = hip.device.load_safetensors(path, dtype=np.float32)
+    np.testing.assert_array_equal(hip.device.to_numpy(wide["w"]), BF16_VALUES)
+
+
+def test_top_k_sampling_matches_oracle_runtime(hip):
+    """Seeded temperature/top-k generation (generate_tinyllama.py:124-143) on
+    the C1 model: the hip runtime copies each logits row to the host
+    (HIPDeviceAdapter.to_numpy) and samples with the same generator as the
+    oracle runtime, so the two draw the same tokens (their float32 logits
+    agree to ~1e-6, far inside any sampling interval of these draws)."""
+    announce("top-k sampling, C1 model, hip vs oracle")
+    from chomikgrad import synthetic
+    from chomikgrad.runtime import LlamaRuntime
+
+    spec = synthetic.TINY
+    weights = synthetic.weights_as_tensors(synthetic.host_weights(spec.config, spec.dtype, seed=0))
+    prompt = synthetic.prompt_ids(spec.config.vocab_size, 16, 0)
+    results = {}
+    for name in ("hip", "cpu"):
+        runtime = LlamaRuntime(spec.config, weights, compiler=name, dtype=spec.dtype)
+        results[name] = runtime.generate(prompt, 24, temperature=0.8, top_k=20, seed=5)
+    assert results["hip"]["generated_token_ids"] == results["cpu"]["generated_token_ids"]
+    greedy = LlamaRuntime(spec.config, weights, compiler="hip", dtype=spec.dtype).generate(prompt, 24)
+    assert greedy["generated_token_ids"] != results["hip"]["generated_token_ids"]  # sampling took effect

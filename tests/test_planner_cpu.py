@@ -384,3 +384,24 @@ def test_mfma_gemv_block_split_plan():
     expected = realize(*outputs, compiler="cpu")
     for value, reference in zip(got, expected):
         np.testing.assert_allclose(np.asarray(value, np.float32), np.asarray(reference, np.float32), rtol=2e-2, atol=2e-2)
+
+
+def test_transposed_causal_mask_is_not_treated_as_causal():
+    """A transposed causal triangle is a view of the same constant with other
+    strides and is anti-causal: the planner must read the mask through the
+    view and keep it, not drop it as a proved causal mask."""
+    from chomikgrad.llama import _tag
+
+    rng = np.random.default_rng(3)
+    T, hd = 24, 64
+    q, k, v = (Tensor(rng.normal(size=(1, 2, T, hd)).astype(np.float16)) for _ in range(3))
+    tri = np.triu(np.full((T, T), -1e4, np.float32), 1).astype(np.float16)[None, None]
+    for mask, causal in ((Tensor(tri), True), (Tensor(tri).transpose(-2, -1), False),
+                         (Tensor(tri[:, :, ::-1, ::-1].copy()), False)):
+        scores = (q @ k.transpose(-2, -1)) / np.sqrt(hd) + mask
+        out = _tag(scores.softmax(axis=-1) @ v, "sdpa", (q, k, v, mask), 1 / np.sqrt(hd))
+        planned, got = model_run([out], dynamic=[q])  # specialised: the mask is a captured constant
+        steps = [s for s in planned.steps if s.kind == K_SDPA]
+        assert len(steps) == 1 and (steps[0].attrs["causal"] is not None) == causal
+        np.testing.assert_allclose(got[0].astype(np.float32), out.numpy(compiler="cpu").astype(np.float32),
+                                   atol=2e-3, rtol=2e-3)

@@ -71,12 +71,18 @@ def test_c2_ctx512_teacher_forced_and_free_running(hip, tinyllama_runtime):
             logits, caches = runtime._decode_step(int(tokens[step]), len(prompt) + step, context, caches)
     print(f"max float16 deviation {max(noise):.4f}; unclear steps {[i for i, c in enumerate(clear) if not c]}",
           flush=True)
-    first_unclear = clear.index(False) if False in clear else len(tokens)
     runs = {}
     for loop in ("reference", "resident"):
         result = runtime.generate(prompt, context - len(prompt), loop=loop)
         runs[loop] = result["generated_token_ids"]
-        assert runs[loop][:first_unclear] == tokens[:first_unclear].tolist(), loop
+        got = runs[loop][:len(tokens)]
+        # Until the first divergence the device was fed the oracle's tokens,
+        # so its rows are the teacher-forced rows above: a divergence may
+        # only happen at a step whose margin is within the float16 noise.
+        diverged = next((i for i, (a, b) in enumerate(zip(got, tokens)) if a != b), None)
+        print(f"{loop} loop: {len(tokens) if diverged is None else diverged} of {len(tokens)} "
+              f"tokens equal the oracle's before any divergence", flush=True)
+        assert diverged is None or not clear[diverged], f"{loop}: diverged at clear step {diverged}"
     # The two loops run the same kernels on the same inputs: all 128 tokens agree.
     assert runs["reference"] == runs["resident"]
     assert len(runs["resident"]) == context - len(prompt)
@@ -90,7 +96,7 @@ def test_c3_prefill_2048_logits_and_caches(hip, tinyllama_runtime):
     prompt = synthetic.prompt_ids(runtime.config.vocab_size, T, 0)
     logits, caches = runtime.prefill(prompt, T)
     program = runtime._prefill_programs[(T, T)][0]
-    assert "flash" in program.source and "gemm" in program.source
+    assert "sdpa" in program.source and "gemm" in program.source  # sdpa: the flash kernel at T >= 16
     row = hip.device.to_numpy(logits).astype(np.float32).reshape(-1)
     deviation, choice = compare_row(row, as_rows(golden), 0)
     if float(golden["margin"]) > 2 * deviation:

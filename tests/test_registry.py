@@ -181,5 +181,11 @@ def test_foreign_registry_runs_on_the_gpu(hip):
     got = program()
     expected = realize(*outputs, compiler="cpu")
     np.testing.assert_allclose(got[0].astype(np.float32), expected[0].astype(np.float32), atol=2e-2, rtol=1e-2)
+    # Cache rows other than the written position are returned bit for bit;
+    # the written row holds RoPE(k) / v from the GEMV, within float16 noise.
+    written = 21
     for value, reference in zip(got[1:], expected[1:]):
-        assert np.mean(value == reference) > 0.99
+        keep = np.arange(value.shape[2]) != written
+        assert np.array_equal(value[:, :, keep], reference[:, :, keep])
+        np.testing.assert_allclose(value[:, :, written].astype(np.float32),
+                                   reference[:, :, written].astype(np.float32), atol=2e-2, rtol=1e-2)

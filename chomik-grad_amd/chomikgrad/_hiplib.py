@@ -60,6 +60,12 @@ SIGNATURES = {
         ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
         ctypes.c_int, ctypes.c_int64,
     ],
+    "chip_greedy_advance_noalloc": [
+        ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+        ctypes.c_int, ctypes.c_int64,
+    ],
     "chip_peak_memory": [ctypes.POINTER(ctypes.c_size_t)],
     "chip_reset_peak_memory": [],
     "chip_event_create": [c_void_pp],

@@ -587,6 +587,70 @@ int launch_greedy_advance(const void* logits, int logits_dtype, int64_t rows, in
   return CHIP_OK;
 }
 
+// ---- allocation-free greedy advance ----------------------------------------
+// The per-row key words and tickets of k_greedy_advance in a file-scope
+// device array instead of the pool that arg_scratch grows with hipMalloc:
+// kNoAllocRows rows at most (8 bytes of key and 4 of ticket per row, 12 KiB
+// in all, held by each device the library runs on until the process ends).
+// Host code never passes ``scratch`` itself to a kernel (in host code the
+// name is a host-side stand-in, not a device address): it uses the address
+// hipGetSymbolAddress returns for the current device, kept per device by
+// noalloc_setup.  The kernel leaves every key word and ticket at zero when
+// it finishes, so the array only needs clearing once, at set-up.  Calls that
+// overlap on one device share the array and race.
+constexpr int64_t kNoAllocRows = 1024;
+constexpr size_t kNoAllocKeyBytes = kNoAllocRows * sizeof(uint64_t);
+constexpr size_t kNoAllocWords = (kNoAllocKeyBytes + kNoAllocRows * sizeof(int)) / sizeof(uint64_t);
+static __device__ __align__(256) uint64_t scratch[kNoAllocWords];
+
+constexpr int kMaxDevices = 64;
+void* g_noalloc_scratch[kMaxDevices] = {};
+
+__global__ void k_zero_words(uint64_t* words, int64_t n) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    words[i] = 0;
+}
+
+// Once per device, with ``device`` current (chip_init): the array's device
+// address, then a clearing kernel queued on ``stream`` (a kernel rather
+// than a memset, so a caller capturing the stream records no memset node).
+int noalloc_setup(int device, hipStream_t stream) {
+  if (device < 0 || device >= kMaxDevices) return set_error(CHIP_EINVAL, "no-alloc scratch: device index out of range");
+  if (g_noalloc_scratch[device]) return CHIP_OK;
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+    return set_error(CHIP_EHIP, "no-alloc scratch: hipGetSymbolAddress failed");
+  hipLaunchKernelGGL(k_zero_words, dim3(8), dim3(256), 0, stream, static_cast<uint64_t*>(ptr),
+                     static_cast<int64_t>(kNoAllocWords));
+  if (hipGetLastError() != hipSuccess) return set_error(CHIP_EHIP, "no-alloc scratch: clearing launch failed");
+  g_noalloc_scratch[device] = ptr;
+  return CHIP_OK;
+}
+
+int launch_greedy_advance_noalloc(const void* logits, int logits_dtype, int64_t rows, int64_t cols,
+                                  void* tokens_out, void* history, int64_t step, void* position,
+                                  void* attention_mask, int64_t mask_row, void* write_mask,
+                                  int64_t write_row, int mask_dtype, int64_t cache_length,
+                                  int device, hipStream_t stream) {
+  if (logits_dtype != F32 && logits_dtype != F16 && logits_dtype != BF16)
+    return set_error(CHIP_EINVAL, "greedy advance: float logits required");
+  if ((attention_mask || write_mask) && mask_dtype != F32 && mask_dtype != F16 && mask_dtype != BF16)
+    return set_error(CHIP_EINVAL, "greedy advance: float masks required");
+  if (rows > kNoAllocRows)
+    return set_error(CHIP_EINVAL, "greedy advance (no-alloc): more rows than the static scratch holds (1024)");
+  if (cols > 0xffffffffLL) return set_error(CHIP_EINVAL, "greedy advance: too many columns");
+  void* base = device >= 0 && device < kMaxDevices ? g_noalloc_scratch[device] : nullptr;
+  if (!base) return set_error(CHIP_EINVAL, "greedy advance (no-alloc): scratch not set up for this device");
+  Advance a{logits, logits_dtype, mask_dtype, cols, static_cast<int32_t*>(tokens_out),
+            static_cast<int32_t*>(history), step, static_cast<int32_t*>(position),
+            attention_mask, mask_row, write_mask, write_row, cache_length, rows,
+            device_error_word(), static_cast<uint64_t*>(base),
+            reinterpret_cast<int*>(static_cast<char*>(base) + kNoAllocKeyBytes)};
+  hipLaunchKernelGGL(k_greedy_advance, arg_grid(rows, cols), dim3(256), 0, stream, a);
+  if (hipGetLastError() != hipSuccess) return set_error(CHIP_EHIP, "greedy advance launch failed");
+  return CHIP_OK;
+}
+
 CHIP_REGISTER_KIND(CHIP_K_RMSNORM, plan_rmsnorm);
 CHIP_REGISTER_KIND(CHIP_K_ROPE, plan_rope);
 CHIP_REGISTER_KIND(CHIP_K_SDPA, plan_sdpa);

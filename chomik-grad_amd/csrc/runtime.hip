@@ -215,7 +215,7 @@ Planner planner_for(int kind) {
 int* device_error_word() { return g_err_dev; }
 hipStream_t library_stream() { return g_stream; }
 
-// Argmax kernels live in k_sample.hip.
+// Argmax kernels live in k_llama.hip.
 int launch_argmax(const void* src, int dtype, int64_t rows, int64_t cols, int64_t* out_dev,
                   hipStream_t stream);
 int launch_greedy_advance(const void* logits, int logits_dtype, int64_t rows, int64_t cols,
@@ -223,6 +223,12 @@ int launch_greedy_advance(const void* logits, int logits_dtype, int64_t rows, in
                           void* attention_mask, int64_t mask_row, void* write_mask,
                           int64_t write_row, int mask_dtype, int64_t cache_length,
                           hipStream_t stream);
+int noalloc_setup(int device, hipStream_t stream);
+int launch_greedy_advance_noalloc(const void* logits, int logits_dtype, int64_t rows, int64_t cols,
+                                  void* tokens_out, void* history, int64_t step, void* position,
+                                  void* attention_mask, int64_t mask_row, void* write_mask,
+                                  int64_t write_row, int mask_dtype, int64_t cache_length,
+                                  int device, hipStream_t stream);
 
 // ------------------------------------------------------------ plans
 struct Fixup {
@@ -279,6 +285,8 @@ int chip_init(int device) {
   HIP_TRY(hipMemset(g_err_dev, 0, 256));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&g_err_host), 256, hipHostMallocDefault));
   int rc = g_staging.init();
+  if (rc) return rc;
+  rc = noalloc_setup(device, g_stream);  // the allocation-free entry points' static scratch
   if (rc) return rc;
   const char* debug = std::getenv("CHOMIK_HIP_DEBUG");
   g_debug = debug && debug[0] && debug[0] != '0';
@@ -661,6 +669,18 @@ int chip_greedy_advance(const void* logits, int logits_dtype, int64_t rows, int6
   return launch_greedy_advance(logits, logits_dtype, rows, cols, tokens_out, history, step,
                                position, attention_mask, mask_row, write_mask, write_row,
                                mask_dtype, cache_length, g_stream);
+}
+
+int chip_greedy_advance_noalloc(const void* logits, int logits_dtype, int64_t rows, int64_t cols,
+                                void* tokens_out, void* history, int64_t step, void* position,
+                                void* attention_mask, int64_t mask_row, void* write_mask,
+                                int64_t write_row, int mask_dtype, int64_t cache_length) {
+  NEED_INIT();
+  if (!logits || !tokens_out || rows <= 0 || cols <= 0)
+    return fail(CHIP_EINVAL, "bad greedy-advance arguments");
+  return launch_greedy_advance_noalloc(logits, logits_dtype, rows, cols, tokens_out, history, step,
+                                       position, attention_mask, mask_row, write_mask, write_row,
+                                       mask_dtype, cache_length, g_device, g_stream);
 }
 
 int chip_peak_memory(size_t* out) {

@@ -170,6 +170,20 @@ int chip_greedy_advance(const void* logits, int logits_dtype, int64_t rows, int6
                         void* attention_mask, int64_t mask_row, void* write_mask,
                         int64_t write_row, int mask_dtype, int64_t cache_length);
 
+/* Allocation-free variant of chip_greedy_advance: same arguments, kernel and
+ * results.  No reference counterpart: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops).  The
+ * per-row key words and tickets live in a static device array of the library
+ * (1024 rows at most, 12 KiB per device, set up and cleared by chip_init)
+ * instead of scratch that chip_greedy_advance allocates on first use; the
+ * call makes no hipMalloc or hipFree.  More than 1024 rows is CHIP_EINVAL.
+ * The array is shared by every call on the device (the kernel leaves it
+ * zeroed): calls that overlap on one device race. */
+int chip_greedy_advance_noalloc(const void* logits, int logits_dtype, int64_t rows, int64_t cols,
+                                void* tokens_out, void* history, int64_t step, void* position,
+                                void* attention_mask, int64_t mask_row, void* write_mask,
+                                int64_t write_row, int mask_dtype, int64_t cache_length);
+
 /* -- memory statistics ---------------------------------------------------------
  * Replaces DeviceAdapter.reset_peak_memory / peak_memory_bytes
  * (lazy.py:147-151; MLX mx.get_peak_memory, mlx_backend.py:98-102). */

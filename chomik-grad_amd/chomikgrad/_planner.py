@@ -744,8 +744,15 @@ class Emitter:
         stage = rows * K * x.itemsize <= GEMV_STAGE_BYTES
         if not stage and (x.row_stride() % vector or (x.offset * x.itemsize) % 16):
             x = self.materialize(x)
+        # The few positions of one sequence (x of shape (1, T, K), 2 <= T <= 8:
+        # a verification block) are computed row-exactly: each row with the
+        # arithmetic the single-token decode step uses, so a verified token
+        # is the one greedy decoding would produce.  Batches of independent
+        # sequences ((B, 1, K)) keep the MFMA kernel.
+        exact = (x.itemsize == 2 and len(x.shape) == 3 and x.shape[0] == 1
+                 and 2 <= x.shape[1] <= 8 and rows == x.shape[1])
         self.add(K_GEMV, [x], [out], segments=[{"w": w, "out": out, "res": None}],
-                 prologue=None, silu=False, rows=rows, K=K)
+                 prologue=None, silu=False, rows=rows, K=K, exact=exact)
         return out
 
     def lower_rms_norm(self, node, args, eps):
@@ -898,6 +905,7 @@ def mfma_gemv(step: Step) -> bool:
     no RMSNorm prologue, the norm stays its own step."""
     x = step.ins[0]
     return (2 <= step.attrs["rows"] <= 16 and x.itemsize == 2 and step.attrs["K"] % 32 == 0
+            and not step.attrs.get("exact")
             and all(seg["w"].shape[0] % 16 == 0 for seg in step.attrs["segments"]))
 
 
@@ -1255,6 +1263,60 @@ def fuse_decode_attention(steps: List[Step], outputs: List[PV], emitter: "Emitte
     return [s for s in steps if id(s) not in removed]
 
 
+def fuse_block_attention(steps: List[Step], outputs: List[PV], emitter: "Emitter") -> List[Step]:
+    """rope(q) + sdpa of a verification block (T = 2..8 query rows of one
+    sequence at positions p .. p + T - 1, head size 64, 16-bit) -> one
+    read-only decode_attention step: the T rows run as T "sequences" over the
+    one cache (batch stride 0), each with the decode step's own arithmetic
+    (the chunk kernel, planned as for one sequence), so a block row equals the
+    single-token step at its position.  The caches are written before by the
+    block's own KV placement steps, which stay."""
+    counts = _consumers(steps, outputs)
+    producer = _producer(steps)
+    removed = set()
+    tickets: Optional[PV] = None
+    partials: Dict[int, PV] = {}
+    for index, step in enumerate(steps):
+        if step.kind != K_SDPA:
+            continue
+        q, K, V, mask = step.ins
+        Bq, H, T, hd = q.shape
+        if Bq != 1 or not 2 <= T <= 8 or hd != 64 or q.itemsize != 2:
+            continue
+        found = producer.get(id(q.storage))
+        if found is None:
+            continue
+        rq = found[1]
+        if rq.kind != K_ROPE or rq.attrs["mode"] != 1 or rq.attrs["offset"] != 0:
+            continue
+        if not q.whole() or counts.get(id(q.storage)) != 1 or rq.ins[0].shape != q.shape:
+            continue
+        if len(K.shape) != 4 or K.shape[0] != 1 or K.shape != V.shape or K.strides != V.strides:
+            continue
+        KV, C = K.shape[1], K.shape[2]
+        if K.strides[2:] != (64, 1) or C < T or H % KV or H // KV not in (1, 2, 4, 8):
+            continue
+        if mask is None or mask.dtype != q.dtype or K.dtype != q.dtype:
+            continue
+        plan = decode_attention_plan(1, KV, C, H // KV, q.itemsize, float(step.attrs["divisor"]))
+        if plan["passes"] not in (1, 2, 4) or plan["chunks"] > DECODE_ATTN_MAX_CHUNKS:
+            continue
+        if tickets is None or tickets.size < T * KV:
+            tickets = emitter.zeros(4 * max(T * KV, 64), "tickets")
+        floats = T * H * plan["chunks"] * 66 if plan["chunks"] > 1 else 1
+        if floats not in partials:
+            partials[floats] = emitter.zeros(4 * floats, "attention_partials")
+        steps[index] = Step(K_DECODE_ATTN,
+                            [rq.ins[0], None, None, rq.ins[1], rq.ins[2], K, V, None, mask, tickets,
+                             partials[floats]],
+                            [step.outs[0]],
+                            {"in_place": False, "table_length": rq.attrs["table_length"], "mode": 3,
+                             "divisor": step.attrs["divisor"], "passes": plan["passes"], "stream_rows": 0,
+                             "unroll": 0, "read_only": True})
+        removed.add(id(rq))
+    return [s for s in steps if id(s) not in removed]
+
+
 def fuse_attention_projection(steps: List[Step], outputs: List[PV]) -> List[Step]:
     """Batch-1 chunk decode attention whose output feeds only the next
     single-row GEMV (the o projection, residual epilogue or none) -> the
@@ -1265,7 +1327,7 @@ def fuse_attention_projection(steps: List[Step], outputs: List[PV]) -> List[Step
         return steps
     counts = _consumers(steps, outputs)
     for index, att in enumerate(steps):
-        if att.kind != K_DECODE_ATTN or att.attrs["passes"] not in (1, 2, 4):
+        if att.kind != K_DECODE_ATTN or att.attrs["passes"] not in (1, 2, 4) or att.attrs.get("read_only"):
             continue
         q, partials = att.ins[0], att.ins[10]
         out = att.outs[0]
@@ -1546,6 +1608,21 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         ints += [ws[0], ws[2], 1 if a["in_place"] else 0] + list(cache.strides)
         ints += [dtype_code(placement.dtype), dtype_code(w.dtype)]
         return kind, [_ptr(cache), _ptr(x), _ptr(placement), _ptr(w), _ptr(out)], ints, []
+    if kind == K_DECODE_ATTN and a.get("read_only"):
+        # T query rows of one block as T sequences over one cache (batch
+        # stride 0): q strides (t, h, d), mask strides (t, h, c)
+        q, _, _, position, table, cache_k, cache_v, _, mask, tickets, partials = step.ins
+        out = step.outs[0]
+        _, H, T, _ = q.shape
+        KV, C = cache_k.shape[1], cache_k.shape[2]
+        ms = broadcast_strides(mask, (1, H, T, C))
+        ints = [T, H, KV, C, dtype_code(q.dtype), q.strides[2], q.strides[1], q.strides[3],
+                0, 0, 0, 0, 0, 0, 3, a["table_length"], 0] + list(cache_k.strides[1:])
+        ints += [0, 0, ms[2], ms[1], ms[3], dtype_code(mask.dtype), dtype_code(q.dtype),
+                 0, a["passes"], 0, 0, 0, 1]
+        ptrs = [_ptr(pv) for pv in (q, None, None, position, table, cache_k, cache_v, None, mask, out, None,
+                                    None, tickets, partials)]
+        return kind, ptrs, ints, [a["divisor"]]
     if kind == K_DECODE_ATTN:
         q, k, v, position, table, cache_k, cache_v, w, mask, tickets, partials = step.ins
         out, out_k, out_v = step.outs
@@ -1560,7 +1637,7 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
                 a["mode"], a["table_length"]] + list(cache_k.strides)
         ints += [ws[0], ws[2], ms[0], ms[1], ms[3], dtype_code(mask.dtype), dtype_code(w.dtype),
                  1 if a["in_place"] else 0, a["passes"], a["stream_rows"], a["unroll"],
-                 1 if a.get("partials_only") else 0]
+                 1 if a.get("partials_only") else 0, 0]
         ptrs = [_ptr(pv) for pv in (q, k, v, position, table, cache_k, cache_v, w, mask, out, out_k, out_v,
                                     tickets, partials)]
         return kind, ptrs, ints, [a["divisor"]]
@@ -1606,7 +1683,8 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         vector = 16 // x.itemsize
         aligned = x.row_stride() % vector == 0 and (_ptr(x)[1] % 16) == 0
         ints += [dtype_code(prologue["w"].dtype) if prologue else 0, 1 if stage else 0, GEMV_SPLIT,
-                 1 if aligned else 0, 0, a.get("blocks", 1), a.get("ticket_bytes", 0)]
+                 1 if aligned else 0, 0, a.get("blocks", 1), a.get("ticket_bytes", 0),
+                 1 if a.get("exact") else 0, 0]
         return kind, ptrs, ints, [prologue["eps"] if prologue else 0.0]
     raise AssertionError(f"no encoder for step kind {kind}")
 
@@ -1659,6 +1737,8 @@ def describe(step: Step, names: Dict[int, str]) -> str:
             tags.append("silu_mul")
         if any(s["res"] is not None for s in a["segments"]):
             tags.append("residual")
+        if a.get("exact"):
+            tags.append("row_exact")
         label += f"[{'+'.join(tags)}]" if tags else ""
         weights = ", ".join(f"{name(s['w'])}{tuple(s['w'].shape)}" for s in a["segments"])
         x = a["prologue"]["x"] if a["prologue"] else step.ins[0]
@@ -1666,6 +1746,8 @@ def describe(step: Step, names: Dict[int, str]) -> str:
                 f"rows={a['rows']}, K={a['K']}, W=[{weights}])")
     if step.kind == K_ELEMENTWISE:
         label = "fused_elementwise" if len(a["ops"]) > 1 else f"elementwise_{a['expression'][0]}"
+    if step.kind == K_DECODE_ATTN and a.get("read_only"):
+        label = "decode_attention[block]"
     ins = ", ".join(name(pv) for pv in step.ins)
     outs = ", ".join(name(pv) for pv in step.outs)
     shape = tuple(step.outs[0].shape) if step.outs else ()
@@ -1693,6 +1775,7 @@ def plan_graph(compiler, outputs: Sequence[LazyNode], dynamic_inputs: Sequence[L
     steps = merge_sibling_gemvs(steps)
     steps = merge_sibling_gemms(steps)
     steps = fuse_decode_attention(steps, out_pvs, emitter)
+    steps = fuse_block_attention(steps, out_pvs, emitter)
     steps = fuse_attention_projection(steps, out_pvs)
     steps = attach_gemv_workspace(steps, emitter)
 

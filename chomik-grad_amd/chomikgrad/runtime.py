@@ -189,6 +189,12 @@ class LlamaRuntime:
     def _verify_block(self, inputs: Sequence[int], position: int, context: int, caches: List[Any]):
         """Run the verification block over ``inputs`` at ``position``: returns
         the target's greedy prediction after each input and the caches."""
+        logits, caches = self._verify_block_logits(inputs, position, context, caches)
+        predictions = np.asarray(self.device.argmax_last_axis(logits)).reshape(-1)
+        return [int(t) for t in predictions], caches
+
+    def _verify_block_logits(self, inputs: Sequence[int], position: int, context: int, caches: List[Any]):
+        """The verification block's logits (1, len(inputs), V) and caches."""
         c = self.config
         block = len(inputs)
         program, nodes = self._verifier(block, context, position, caches)
@@ -203,8 +209,7 @@ class LlamaRuntime:
             *caches,
         ]
         native = program.run(dict(zip(nodes, values)), synchronize=False)
-        predictions = np.asarray(self.device.argmax_last_axis(native[0])).reshape(-1)
-        return [int(t) for t in predictions], list(native[1:])
+        return native[0], list(native[1:])
 
     def generate_speculative(
         self,

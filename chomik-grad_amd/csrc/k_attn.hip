@@ -211,8 +211,14 @@ __device__ __forceinline__ void combine_chunks(const KArgs& a, int64_t b, int64_
 // mask strides (b, h, c), n[25] mask dtype, n[26] w dtype (both must be the
 // model dtype), n[27] in place, n[28] passes per workgroup NP (1, 2 or 4),
 // n[31] partials only (with NS > 1: the next step, the output projection,
-// combines them and p[9] is not written); f[0] score divisor (sqrt(hd) before
-// rounding).
+// combines them and p[9] is not written); n[32] read only: the caches were
+// updated before (a verification block's KV placement), p[1], p[2], p[7],
+// p[10] and p[11] are unused and nothing is written but the output; position
+// mode 3 is then position[0] + b, the "sequences" being the T query rows of
+// one block over one cache (cache batch stride 0); f[0] score divisor
+// (sqrt(hd) before rounding).  A query row's arithmetic does not depend on
+// B, so each row of a block equals the single-token decode step at its
+// position bit for bit.
 template <typename T, int G, int NP>
 __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
   using E = Elem<T>;
@@ -244,12 +250,13 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
   const int64_t mb = b * a.n[22], mhs = a.n[23], mc = a.n[24];
   const bool masked = a.p[8] != nullptr;
   const bool in_place = a.n[27] != 0;
+  const bool writes = a.n[32] == 0;
   const T* Wm = static_cast<const T*>(a.p[7]);
   const T* Am = static_cast<const T*>(a.p[8]);
 
   // -- issue: position, q/k/v, this chunk's K and V rows, w and mask values.
   const int32_t* positions = static_cast<const int32_t*>(a.p[3]);
-  int64_t pos = a.n[14] == 2 ? positions[b] : positions[0];
+  int64_t pos = a.n[14] == 2 ? positions[b] : positions[0] + (a.n[14] == 3 ? b : 0);
   float xq[QT];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
     xq[t] = i < G * kHead ? load_f(a.p[0], b * a.n[5] + (g * G + i / kHead) * a.n[6] + lane * a.n[7], dt) : 0.f;
   }
   float xk = 0.f, xv = 0.f;
-  if (tid < kHead) {
+  if (tid < kHead && writes) {
     xk = load_f(a.p[1], b * a.n[8] + g * a.n[9] + tid * a.n[10], dt);
     xv = load_f(a.p[2], b * a.n[11] + g * a.n[12] + tid * a.n[13], dt);
   }
@@ -272,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
     const int64_t off = cb + (in ? j : 0) * cs;
     kraw[u] = in ? reinterpret_cast<const uint4*>(Kc + off)[part] : make_uint4(0, 0, 0, 0);
     vraw[u] = in ? reinterpret_cast<const uint4*>(Vc + off)[part] : make_uint4(0, 0, 0, 0);
-    wj[u] = in ? E::to_f(Wm[wb + j * wc]) : 0.f;
+    wj[u] = (in && writes) ? E::to_f(Wm[wb + j * wc]) : 0.f;
     mk[u] = (in && masked) ? E::to_f(Am[mb + (g * G + head) * mhs + j * mc]) : 0.f;
   }
 
@@ -441,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_attn(KArgs a) {
 #pragma unroll
   for (int u = 0; u < NP; ++u) {
     const int64_t j = c0 + rg + u * RPP;
-    if (j >= C) continue;
+    if (j >= C || !writes) continue;
     const float w = wj[u];
     if (in_place && w == 0.f) continue;
     uint4 kvec = kraw[u], vvec = vraw[u];
@@ -1200,9 +1207,11 @@ const char* plan_decode_attn(KArgs& a, Launch& l) {
   const int64_t B = a.n[0], H = a.n[1], KV = a.n[2], C = a.n[3];
   if (B <= 0 || H <= 0 || KV <= 0 || C <= 0 || H % KV) return "decode_attn: bad shape";
   if (a.n[18] != kHead || a.n[19] != 1) return "decode_attn: cache rows must be contiguous 64-element rows";
-  if (a.n[14] != 1 && a.n[14] != 2) return "decode_attn: position input required";
+  if (a.n[14] < 1 || a.n[14] > 3) return "decode_attn: position input required";
   if (a.n[25] != a.n[4] || a.n[26] != a.n[4]) return "decode_attn: masks must have the model dtype";
   const int np = static_cast<int>(a.n[28]);
+  if ((a.n[14] == 3 || a.n[32] != 0) && ((np != 1 && np != 2 && np != 4) || a.n[31] != 0))
+    return "decode_attn: read-only block rows run on the chunk kernel only";
   if (np == 8) {  // MFMA kernel: one workgroup per (sequence, KV head), n[29] blocks per wave
     const int nb = static_cast<int>(a.n[29]);
     if (a.n[4] != F16 && a.n[4] != BF16) return "decode_attn: the MFMA kernel needs a 16-bit cache";

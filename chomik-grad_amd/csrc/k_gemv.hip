@@ -1264,6 +1264,214 @@ const char* plan_attn_proj(KArgs& a, Launch& l) {
   return nullptr;
 }
 
+// Row-exact few-row GEMV (2..8 rows of a 16-bit type, the positions of one
+// sequence: a speculative verification block).  Every output row is computed
+// with exactly the arithmetic of the single-row decode kernel the same
+// matrix gets at M = 1 -- k_gemv_row's one chain per lane, or, for the
+// matrices k_gemv_stream serves (n[27] = 1), its two chains -- with the same
+// lane -> column map (lane + 64 u), the same RMSNorm prologue, the same wave
+// reduction and the same epilogue.  A verification block's rows therefore
+// equal the decode step's bit for bit, which is what makes speculative
+// decoding reproduce greedy decoding token for token.  The x rows are staged
+// in LDS once per block; each wave owns one row group (a row, or the gate/up
+// pair), keeps its weight vectors in registers and walks the M rows.  Same
+// KArgs layout as k_gemv; n[27] two chains.
+// Blocks of 8 waves, or 4 (one per SIMD, up to 512 registers) for the widest
+// rows, whose weight and x vectors would not fit 256.
+constexpr int exact_threads(int vpl) { return vpl >= 11 ? 256 : 512; }
+
+template <typename T, int VPL, bool FULL>
+__global__ __launch_bounds__(exact_threads(VPL)) void k_gemv_exact(KArgs a) {
+  using E = Elem<T>;
+  using W = Word<T>;
+  constexpr int V = 16 / sizeof(T);
+  extern __shared__ uint4 xs[];  // M x KV vectors of x
+  const int M = static_cast<int>(a.n[0]);
+  const int64_t K = a.n[1];
+  const int KV = static_cast<int>(K / V);
+  const bool pro = a.n[5] == 1, silu = a.n[6] != 0, two = a.n[27] != 0;
+  const int RG = silu ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  {  // stage x (rows at stride n[2] elements, 16-byte aligned)
+    const uint4* xg = static_cast<const uint4*>(a.p[0]);
+    const int64_t xstride = a.n[2] / V;
+    for (int i = threadIdx.x; i < M * KV; i += blockDim.x) xs[i] = xg[(i / KV) * xstride + i % KV];
+  }
+  __syncthreads();
+
+  const int64_t wave = blockIdx.x * int64_t(blockDim.x >> 6) +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const Segments<T> st(a);
+  const int64_t groups = silu ? a.n[7] : st.total;
+  if (wave >= groups) return;  // no barrier below
+  const uint4* wrow[2];
+  int seg[2];
+  int64_t idx[2];
+  if (silu) {
+    wrow[0] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2]) + wave * K);
+    wrow[1] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[3]) + wave * K);
+    seg[0] = 0;
+    seg[1] = 1;
+    idx[0] = idx[1] = wave;
+  } else {
+    seg[0] = seg[1] = st.seg_of(wave);
+    idx[0] = idx[1] = wave - st.start(seg[0]);
+    wrow[0] = wrow[1] = reinterpret_cast<const uint4*>(st.weight(seg[0]) + idx[0] * K);
+  }
+  const uint4* ng = static_cast<const uint4*>(a.p[1]);
+  const int chunks = FULL ? 1 : (KV + 64 * VPL - 1) / (64 * VPL);
+
+  float acc[kMaxRows][2], acc2[kMaxRows][2];
+#pragma unroll
+  for (int m = 0; m < kMaxRows; ++m)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) acc[m][r] = acc2[m][r] = 0.f;
+
+  for (int chunk = 0; chunk < chunks; ++chunk) {
+    const int base = chunk * 64 * VPL + lane;
+    uint4 wv[2][VPL], nv[VPL];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const int c = base + 64 * u;
+        if (r < RG && (FULL || c < KV)) {
+          wv[r][u] = load_w<true>(wrow[r] + c);
+        } else {
+          wv[r][u] = zero;
+        }
+      }
+#pragma unroll
+    for (int u = 0; u < VPL; ++u) {
+      const int c = base + 64 * u;
+      nv[u] = (pro && (FULL || c < KV)) ? load_x(ng + c) : zero;
+    }
+    // m unrolled to constant indices (a runtime index would put acc in
+    // private memory)
+#pragma unroll
+    for (int m = 0; m < kMaxRows; ++m) {
+      if (m >= M) break;
+      uint32_t xw[VPL][4];
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const int c = base + 64 * u;
+        const uint4 v = (FULL || c < KV) ? xs[m * KV + c] : zero;
+        xw[u][0] = v.x;
+        xw[u][1] = v.y;
+        xw[u][2] = v.z;
+        xw[u][3] = v.w;
+      }
+      if (pro) {  // one chunk covers K (the planner admits the prologue only then)
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < VPL; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[u][i], xw[u][i]), W::kOnes, ss);
+        const float total = E::round(wave_sum(ss));
+        const float mean = E::round(total / E::round(static_cast<float>(K)));
+        const float rn = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+        const float inv = 1.0f / rn;
+        bool fast = W::fast_divisor(rn);
+        if constexpr (!W::kNoBranch) {
+#pragma unroll
+          for (int u = 0; u < VPL; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              fast = fast && W::fast_numerator(W::lo(xw[u][i])) && W::fast_numerator(W::hi(xw[u][i]));
+          fast = __all(fast);
+        }
+#pragma unroll
+        for (int u = 0; u < VPL; ++u) {
+          const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = W::lo(xw[u][i]), hi = W::hi(xw[u][i]);
+            float ql, qh;
+            if constexpr (W::kNoBranch) {
+              ql = fast ? quotient(lo, rn, inv) : lo * inv;
+              qh = fast ? quotient(hi, rn, inv) : hi * inv;
+            } else {
+              ql = fast ? quotient(lo, rn, inv) : lo / rn;
+              qh = fast ? quotient(hi, rn, inv) : hi / rn;
+            }
+            xw[u][i] = W::mul(W::pack(ql, qh), nw[i]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        if (r >= RG) break;
+        float s0 = acc[m][r], s1 = acc2[m][r];
+        if (two) {  // k_gemv_stream: elements 0, 2 of a vector on one chain, 1, 3 on the other
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) {
+            const uint32_t ww[4] = {wv[r][u].x, wv[r][u].y, wv[r][u].z, wv[r][u].w};
+            s0 = W::dot(xw[u][0], ww[0], s0);
+            s1 = W::dot(xw[u][1], ww[1], s1);
+            s0 = W::dot(xw[u][2], ww[2], s0);
+            s1 = W::dot(xw[u][3], ww[3], s1);
+          }
+        } else {  // k_gemv_row: one chain in (u, i) order
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) {
+            const uint32_t ww[4] = {wv[r][u].x, wv[r][u].y, wv[r][u].z, wv[r][u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s0 = W::dot(xw[u][i], ww[i], s0);
+          }
+        }
+        acc[m][r] = s0;
+        acc2[m][r] = s1;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < kMaxRows; ++m) {
+    if (m >= M) break;
+    float y[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) y[r] = r < RG ? wave_sum(two ? acc[m][r] + acc2[m][r] : acc[m][r]) : 0.f;
+    if (silu) {
+      const float g = E::round(y[0]);
+      const float u = E::round(y[1]);
+      const float denom = E::round(E::round(expf(-g)) + 1.f);
+      const T out = E::from_f(E::round(E::round(g / denom) * u));
+      if (lane == 0) static_cast<T*>(a.p[6])[m * a.n[11] + idx[0]] = out;
+    } else {
+      float v = E::round(y[0]);
+      const T* res = st.residual(seg[0]);
+      if (res) v = E::round(E::to_f(res[m * st.res_stride(seg[0]) + idx[0]]) + v);
+      if (lane == 0) st.output(seg[0])[m * st.out_stride(seg[0]) + idx[0]] = E::from_f(v);
+    }
+  }
+}
+
+// The (VPL, FULL) the M = 1 kernel of this matrix uses: k_gemv_stream's exact
+// fits (pick_stream) with two chains, else k_gemv_row's (pick_row_nt).
+template <typename T>
+const void* pick_exact(int64_t kv, bool pro, bool silu, bool two) {
+  if (kv % 64 == 0) {
+    const int64_t per_lane = kv / 64;
+    const bool fits = per_lane == 1 || per_lane == 2 || per_lane == 4 || per_lane == 8 ||
+                      (per_lane == 11 && !silu) || (per_lane == 16 && !silu && !pro);
+    if (fits) {
+      switch (per_lane) {
+        case 1: return reinterpret_cast<const void*>(&k_gemv_exact<T, 1, true>);
+        case 2: return reinterpret_cast<const void*>(&k_gemv_exact<T, 2, true>);
+        case 4: return reinterpret_cast<const void*>(&k_gemv_exact<T, 4, true>);
+        case 8: return reinterpret_cast<const void*>(&k_gemv_exact<T, 8, true>);
+        case 11: return reinterpret_cast<const void*>(&k_gemv_exact<T, 11, true>);
+        default: return reinterpret_cast<const void*>(&k_gemv_exact<T, 16, true>);
+      }
+    }
+  }
+  return two ? nullptr : reinterpret_cast<const void*>(&k_gemv_exact<T, 4, false>);
+}
+
+constexpr size_t kExactStageBytes = 64 * 1024;
+
 const char* plan_gemv(KArgs& a, Launch& l) {
   const int64_t M = a.n[0], K = a.n[1];
   const int dt = static_cast<int>(a.n[3]);
@@ -1295,16 +1503,42 @@ const char* plan_gemv(KArgs& a, Launch& l) {
   const bool row_ok = M == 1 && aligned && (!pro || (a.n[19] == dt && one_pass));
   // 0: never stream, 1: stream large matrices, 2: stream every exact fit
   static const int stream_knob = env_int("CHOMIK_HIP_GEMV_STREAM", 1);
-  if (row_ok && stream_knob && (dt == F16 || dt == BF16)) {
-    const void* func = dt == F16 ? pick_stream<__half>(kv, pro, silu) : pick_stream<bf16_t>(kv, pro, silu);
-    // about eight waves per CU: as many row groups per wave as that takes,
-    // then as few waves as those groups need (balanced runs).  Only worth it
-    // from 8 groups per wave (the lm_head): below that one wave per row with
-    // every load issued at once (k_gemv_row) finishes sooner.
-    static const int target = env_int("CHOMIK_HIP_GEMV_TARGET_WAVES", 2048);
+  // about eight waves per CU: as many row groups per wave as that takes,
+  // then as few waves as those groups need (balanced runs).  Only worth it
+  // from 8 groups per wave (the lm_head): below that one wave per row with
+  // every load issued at once (k_gemv_row) finishes sooner.
+  static const int target = env_int("CHOMIK_HIP_GEMV_TARGET_WAVES", 2048);
+  const void* stream_func = nullptr;
+  bool stream_pick = false;  // whether M = 1 takes k_gemv_stream for this matrix
+  if (stream_knob && (dt == F16 || dt == BF16)) {
+    stream_func = dt == F16 ? pick_stream<__half>(kv, pro, silu) : pick_stream<bf16_t>(kv, pro, silu);
     const int64_t groups = silu ? a.n[7] : rows;
     const int64_t per_wave = (groups + target - 1) / target;
-    if (func && (per_wave >= 8 || stream_knob == 2)) {
+    stream_pick = stream_func && (per_wave >= 8 || stream_knob == 2);
+  }
+  // Row-exact few rows (n[26], the positions of one sequence): each row with
+  // the arithmetic of the kernel this matrix gets at M = 1.
+  const size_t exact_bytes = static_cast<size_t>(M * K) * dtype_size(dt);
+  if (a.n[26] != 0 && M >= 2 && (dt == F16 || dt == BF16) && aligned &&
+      (!pro || (a.n[19] == dt && one_pass)) && exact_bytes <= kExactStageBytes) {
+    const int64_t groups = silu ? a.n[7] : rows;
+    const int threads = exact_threads(static_cast<int>(kv % 64 == 0 ? kv / 64 : 4));
+    const int64_t blocks = (groups + threads / 64 - 1) / (threads / 64);
+    if (blocks > 2147483647) return "gemv: too many rows";
+    a.n[27] = stream_pick ? 1 : 0;
+    l.func = dt == F16 ? pick_exact<__half>(kv, pro, silu, stream_pick)
+                       : pick_exact<bf16_t>(kv, pro, silu, stream_pick);
+    if (!l.func) return "gemv: no row-exact kernel for this width";
+    l.grid = dim3(static_cast<unsigned>(blocks));
+    l.block = dim3(threads);
+    l.shmem = exact_bytes;
+    return nullptr;
+  }
+  if (row_ok && stream_pick) {
+    const void* func = stream_func;
+    const int64_t groups = silu ? a.n[7] : rows;
+    const int64_t per_wave = (groups + target - 1) / target;
+    {
       const int64_t waves = (groups + per_wave - 1) / per_wave;
       if ((waves + 3) / 4 > 2147483647) return "gemv: too many rows";
       a.n[23] = waves;

@@ -482,7 +482,11 @@ def s_decode_attn(mem, p, n, f):
     qs, ks, vs = n[5:8], n[8:11], n[11:14]
     mode, length = n[14], n[15]
     cs = n[16:20]
-    wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes, stream_rows, unroll, partials_only = n[20:32]
+    wsb, wsc, msb, msh, msc, mdt, wdt, in_place, passes, stream_rows, unroll, partials_only, read_only = n[20:33]
+    # read only: T query rows of one block over one already-updated cache
+    # (cache batch stride 0, positions position[0] + b, nothing written but
+    # the output); only on the chunk kernel
+    assert not read_only or (passes in (1, 2, 4) and mode == 3 and cs[0] == 0 and not partials_only)
     assert (passes in (1, 2, 4) or (passes == 0 and stream_rows > 0 and unroll in (2, 4))
             or (passes == 8 and dt in (1, 2) and 1 <= stream_rows <= 3 and -(-C // 32) <= 8 * stream_rows))
     rpp = 16 if dt == 0 else 32
@@ -503,7 +507,7 @@ def s_decode_attn(mem, p, n, f):
     d = np.arange(64)
     newk = {}
     for b in range(B):
-        pos = int(mem.view(p[3], 3, B if mode == 2 else 1)[b if mode == 2 else 0])
+        pos = int(mem.view(p[3], 3, B if mode == 2 else 1)[b if mode == 2 else 0]) + (b if mode == 3 else 0)
         if not 0 <= pos < length:
             error |= 2
             pos = 0
@@ -513,11 +517,14 @@ def s_decode_attn(mem, p, n, f):
         def rope(x):
             return _round(np.concatenate([x[:32] * c + x[32:] * -s, x[:32] * s + x[32:] * c]), dt)
 
-        w = load(mem, p[7], wdt, b * wsb + np.arange(C) * wsc)
+        w = np.zeros(C, np.float32) if read_only else load(mem, p[7], wdt, b * wsb + np.arange(C) * wsc)
         keep = _round(1 - w, dt)[:, None]
         for g in range(KV):
-            k = rope(load(mem, p[1], dt, b * ks[0] + g * ks[1] + d * ks[2]))
-            v = load(mem, p[2], dt, b * vs[0] + g * vs[1] + d * vs[2])
+            if read_only:
+                k = v = np.zeros(64, np.float32)
+            else:
+                k = rope(load(mem, p[1], dt, b * ks[0] + g * ks[1] + d * ks[2]))
+                v = load(mem, p[2], dt, b * vs[0] + g * vs[1] + d * vs[2])
             idx = b * cs[0] + g * cs[1] + np.arange(C)[:, None] * cs[2] + d[None, :] * cs[3]
             Kc, Vc = load(mem, p[5], dt, idx), load(mem, p[6], dt, idx)
             Kn = np.where(w[:, None] != 0, _round(_round(Kc * keep, dt) + _round(k[None] * w[:, None], dt), dt), Kc)
@@ -537,6 +544,8 @@ def s_decode_attn(mem, p, n, f):
                     else:
                         store(mem, p[9], dt, (b * H + h) * 64 + d, out)
     for (b, g), (idx, Kn, Vn, w) in newk.items():
+        if read_only:
+            continue
         if in_place:
             rows = w != 0
             store(mem, p[10], dt, idx[rows].reshape(-1), Kn[rows].reshape(-1))

@@ -126,14 +126,22 @@ def test_structural_program_cache_and_leaf_aliasing(hip):
     np.testing.assert_allclose((left + right).numpy(compiler="hip"), [11.0, 22.0])
 
 
+@pytest.mark.parametrize("layout", ["sequence", "batch"])
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, BFLOAT16])
 @pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
-def test_gemv_linear_variants(hip, dtype, rows):
-    announce(f"gemv {np.dtype(dtype)} rows={rows}")
+def test_gemv_linear_variants(hip, dtype, rows, layout):
+    """Few-row linears with RMSNorm prologue, residual and SiLU-pair
+    epilogues against the oracle.  ``sequence``: x of shape (1, rows, K), the
+    positions of one sequence (the row-exact kernel for 16-bit types);
+    ``batch``: (rows, 1, K), independent sequences (the MFMA kernel)."""
+    if layout == "batch" and rows == 1:
+        pytest.skip("one row: the same graph as the sequence layout")
+    announce(f"gemv {np.dtype(dtype)} rows={rows} {layout}")
     rng = np.random.default_rng(rows)
     K, N = 512, 384
-    x = Tensor(rng.normal(size=(1, rows, K)).astype(np.float32), dtype=dtype)
-    h = Tensor(rng.normal(size=(1, rows, N)).astype(np.float32), dtype=dtype)
+    shape = (1, rows) if layout == "sequence" else (rows, 1)
+    x = Tensor(rng.normal(size=shape + (K,)).astype(np.float32), dtype=dtype)
+    h = Tensor(rng.normal(size=shape + (N,)).astype(np.float32), dtype=dtype)
     norm = Tensor(np.ones(K, np.float32), dtype=dtype)
     w1 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
     w2 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
@@ -166,12 +174,12 @@ def test_gemv_split_over_blocks(hip, dtype, rows, K, N):
 
     announce(f"gemv split {np.dtype(dtype)} rows={rows} K={K} N={N}")
     rng = np.random.default_rng(K + rows)
-    x = Tensor(rng.normal(size=(1, rows, K)).astype(np.float32), dtype=dtype)
-    h = Tensor(rng.normal(size=(1, rows, N)).astype(np.float32), dtype=dtype)
+    x = Tensor(rng.normal(size=(rows, 1, K)).astype(np.float32), dtype=dtype)  # a batch of sequences
+    h = Tensor(rng.normal(size=(rows, 1, N)).astype(np.float32), dtype=dtype)
     w1 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
     w2 = Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype)
     # a GEMV of another width on its own input shares the workspace
-    z = Tensor(rng.normal(size=(1, rows, K)).astype(np.float32), dtype=dtype)
+    z = Tensor(rng.normal(size=(rows, 1, K)).astype(np.float32), dtype=dtype)
     w3 = Tensor((rng.normal(size=(160, K)) * 0.05).astype(np.float32), dtype=dtype)
     gate = x @ w1.T
     outputs = [x @ w2.T, h + (x @ w1.T), gate / (1 + (-gate).exp()) * (x @ w2.T), z @ w3.T]

@@ -359,20 +359,20 @@ def test_decode_attention_plan_limits(B, KV, C, G, itemsize, monkeypatch):
 
 
 def test_mfma_gemv_block_split_plan():
-    """Narrow MFMA GEMVs share each 16-column tile among several blocks over
-    K, with one zero-initialised workspace (tickets, then the partial tiles)
+    """Narrow MFMA GEMVs (a batch of 8 sequences) share each 16-column tile
+    among several blocks over K, with one zero-initialised workspace (tickets, then the partial tiles)
     sized for the largest; wide or short-K ones stay unsplit; the planned
     program computes the portable chain's values."""
     from chomikgrad import _planner
 
     rng = np.random.default_rng(3)
-    x = Tensor(rng.normal(size=(1, 8, 8192)).astype(np.float32), dtype=np.float16)
-    h = Tensor(rng.normal(size=(1, 8, 384)).astype(np.float32), dtype=np.float16)
+    x = Tensor(rng.normal(size=(8, 1, 8192)).astype(np.float32), dtype=np.float16)
+    h = Tensor(rng.normal(size=(8, 1, 384)).astype(np.float32), dtype=np.float16)
     narrow = Tensor((rng.normal(size=(384, 8192)) * 0.02).astype(np.float32), dtype=np.float16)
     wide = Tensor((rng.normal(size=(8192, 2048)) * 0.05).astype(np.float32), dtype=np.float16)
     short = Tensor((rng.normal(size=(384, 256)) * 0.05).astype(np.float32), dtype=np.float16)
-    y = Tensor(rng.normal(size=(1, 8, 256)).astype(np.float32), dtype=np.float16)
-    z = Tensor(rng.normal(size=(1, 8, 2048)).astype(np.float32), dtype=np.float16)
+    y = Tensor(rng.normal(size=(8, 1, 256)).astype(np.float32), dtype=np.float16)
+    z = Tensor(rng.normal(size=(8, 1, 2048)).astype(np.float32), dtype=np.float16)
     outputs = [h + x @ narrow.T, z @ wide.T, y @ short.T]  # distinct inputs: no sibling merge
     planned, got = model_run(outputs)
     gemvs = {s.attrs["segments"][0]["w"].shape: s for s in planned.steps if s.kind == K_GEMV}
@@ -405,3 +405,40 @@ def test_transposed_causal_mask_is_not_treated_as_causal():
         assert len(steps) == 1 and (steps[0].attrs["causal"] is not None) == causal
         np.testing.assert_allclose(got[0].astype(np.float32), out.numpy(compiler="cpu").astype(np.float32),
                                    atol=2e-3, rtol=2e-3)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+def test_verify_block_plans_row_exact_kernels(dtype):
+    """A verification block (5 positions of one sequence, LlamaDecoderBlock):
+    its linears are planned row-exact (the single-token step's arithmetic
+    per row, RMSNorm as the prologue) and its attention as the read-only
+    decode attention over the placed caches (the decode step's kernel, one
+    "sequence" per block row); the tape computes the oracle's values."""
+    config = LlamaConfig(vocab_size=300, hidden_size=512, intermediate_size=1376, num_hidden_layers=2,
+                         num_attention_heads=8, num_key_value_heads=4, max_position_embeddings=128)
+    weights = synthetic.weights_as_tensors(synthetic.host_weights(config, dtype, seed=13))
+    C, position, block = 90, 37, 5
+    placement, write, attention = block_masks(position, block, C, dtype)
+    leaves = [Tensor(np.array([[4, 250, 17, 99, 3]], np.int32), copy=False),
+              Tensor(_rope_rotations(block, 64, config.rope_theta, dtype, offset=position), copy=False),
+              Tensor(attention, copy=False), Tensor(placement, copy=False), Tensor(write, copy=False),
+              Tensor(np.asarray(position, np.int32), copy=False)]
+    rng = np.random.default_rng(8)
+    caches = [Tensor(as_dtype_host(rng.normal(0, 0.5, (1, 4, C, 64)), dtype), copy=False) for _ in range(4)]
+    step = LlamaDecoderBlock(config, weights, block_length=block, cache_length=C, dtype=dtype)
+    outputs = step(*leaves[:5], list(zip(caches[::2], caches[1::2])), position=leaves[5])
+    expected = realize(*outputs, compiler="cpu")
+    planned, got = model_run(outputs, leaves + caches, donate=caches)
+    source = planned.source
+    assert source.count("decode_attention[block]") == 2 and " sdpa(" not in source
+    assert source.count("gemv[rms_norm+row_exact]") == 3  # q/k/v of 2 layers + lm_head
+    assert source.count("gemv[rms_norm+silu_mul+row_exact]") == 2
+    assert source.count("gemv[residual+row_exact]") == 4
+    np.testing.assert_allclose(as_float(got[0]), as_float(expected[0]), atol=3e-2, rtol=2e-2)
+    for value, reference in zip(got[1:], expected[1:]):
+        np.testing.assert_allclose(as_float(value), as_float(reference), atol=3e-2, rtol=2e-2)
+
+
+def as_dtype_host(values, dtype):
+    from chomikgrad.dtypes import as_dtype
+    return as_dtype(np.asarray(values, np.float32), dtype)

@@ -148,6 +148,26 @@ class HIPDeviceAdapter(DeviceAdapter):
                           host.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(host.nbytes), 1)
         return result
 
+    def upload(self, dst: HIPArray, value: object) -> None:
+        """Queue a copy of a host array into an existing device array of the
+        same size (staged through pinned memory; the host array may be reused
+        at once).  No allocation, so a loop's bound inputs keep their
+        addresses."""
+        host = np.ascontiguousarray(as_dtype(np.asarray(value), dst.dtype))
+        if host.nbytes != dst.nbytes:
+            raise ValueError(f"upload of {host.nbytes} bytes into a {dst.nbytes}-byte array")
+        if host.nbytes:
+            self.lib.call("chip_memcpy_h2d", ctypes.c_void_p(dst.ptr), host.ctypes.data_as(ctypes.c_void_p),
+                          ctypes.c_size_t(host.nbytes), 1)
+
+    def view(self, base: HIPArray, offset: int, shape: Sequence[int]) -> HIPArray:
+        """Elements ``offset .. offset + prod(shape)`` of ``base`` as an array
+        of ``shape`` (no copy; keeps ``base`` alive)."""
+        count = int(np.prod(shape, dtype=np.int64))
+        if offset < 0 or offset + count > base.size:
+            raise ValueError("view outside its base array")
+        return HIPArray(base.ptr + offset * base.dtype.itemsize, shape, base.dtype, base=base, lib=self.lib)
+
     def zeros(self, shape: Sequence[int], dtype: object) -> HIPArray:
         result = self.empty(shape, dtype)
         if result.ptr:

@@ -221,6 +221,7 @@ class LlamaRuntime:
         draft_prompt: Optional[Sequence[int]] = None,
         bonus: bool = False,
         stop_at_eos: bool = False,
+        loop: Optional[str] = None,
     ) -> Dict[str, object]:
         """Greedy speculative decoding with ``draft`` proposing for this
         (target) runtime -- the reference's _generate_speculative_loaded
@@ -240,7 +241,11 @@ class LlamaRuntime:
         the target's prediction after ``dk`` is emitted as well, and the
         draft, which never consumed ``dk``, catches up with one extra step
         before its next proposal.  Either way the emitted sequence equals the
-        target's own greedy decoding."""
+        target's own greedy decoding.
+
+        ``loop="reference"`` drives every step from the host, as the
+        reference does; ``loop="resident"`` (the default on the hip plugin)
+        keeps a round on the device and synchronises once per round."""
         from .generation import verify_greedy_candidates
 
         if max_new_tokens <= 0:
@@ -256,6 +261,13 @@ class LlamaRuntime:
             if length > runtime.config.max_position_embeddings:
                 raise ValueError(f"prompt plus output is {length} tokens, model limit is "
                                  f"{runtime.config.max_position_embeddings}")
+        if loop is None:
+            loop = "resident" if self.compiler_name == "hip" and draft.compiler_name == "hip" else "reference"
+        if loop == "resident":
+            return self._speculative_resident(draft, prompt, draft_prompt, max_new_tokens, speculative_tokens,
+                                              bonus, stop_at_eos, context, draft_context)
+        if loop != "reference":
+            raise ValueError(f"unknown loop {loop!r}")
         eos = self.config.eos_token_id
         started = time.perf_counter()
         with no_grad():
@@ -308,6 +320,137 @@ class LlamaRuntime:
         decode_tokens = len(generated) - 1
         return {
             "loop": "speculative" + ("-bonus" if bonus else ""),
+            "generated_token_ids": generated,
+            "prompt_tokens": len(prompt),
+            "generated_tokens": len(generated),
+            "first_token_seconds": first_token_seconds,
+            "decode_seconds": decode_seconds,
+            "warm_tokens_per_second": decode_tokens / decode_seconds if decode_tokens else None,
+            "wall_generation_seconds": time.perf_counter() - started,
+            "fixed_context_tokens": context,
+            "speculative_tokens": speculative_tokens,
+            "accepted_draft_tokens": accepted,
+            "proposed_draft_tokens": proposed,
+            "acceptance_rate": accepted / proposed if proposed else 0.0,
+            "target_verification_calls": verifications,
+            "draft_decode_calls": draft_calls,
+            "kv_cache": True,
+        }
+
+    def _speculative_resident(self, draft, prompt, draft_prompt, max_new_tokens, speculative_tokens, bonus,
+                              stop_at_eos, context, draft_context):
+        """One host synchronisation per round: the draft's proposals feed its
+        next step on the device (greedy_advance writes each token into the
+        draft's input and into the verification block's token row), the
+        block's per-row greedy predictions stay on the device, and the host
+        reads back only the block's tokens and predictions to apply the
+        acceptance rule.  Masks and positions of a round follow from the
+        round's start position, which the host knows, and are uploaded
+        without waiting.  Same tokens as the reference loop."""
+        from .generation import verify_greedy_candidates
+
+        device = draft.device
+        eos = self.config.eos_token_id
+        k = speculative_tokens
+        width = k + 1 if bonus else k  # block rows: [last, d1 .. dk] or [last, d1 .. d_{k-1}]
+        started = time.perf_counter()
+        with no_grad():
+            logits, target_caches = self.prefill(prompt, context)
+            token = device.argmax(logits)
+            first_token_seconds = time.perf_counter() - started
+            _, draft_caches = draft.prefill(draft_prompt, draft_context)
+            generated = [token]
+            decode_started = time.perf_counter()
+            # device state of the draft loop and of the block
+            proposals = device.empty((1, k + 1), np.int32)  # [last, d1 .. dk]
+            block_tokens = device.view(proposals, 0, (1, width))
+            draft_token = device.empty((1, 1), np.int32)
+            draft_pos = device.empty((), np.int32)
+            d_attention_host, d_write_host = decode_masks(0, draft_context, draft.dtype)
+            d_attention = device.array(d_attention_host)
+            d_write = device.array(d_write_host)
+            d_program, d_nodes = draft._decoder(draft_context, len(draft_prompt), draft_caches, donate=True)
+            d_logits = device.empty(d_program._planned.output_nodes[0].shape, draft.dtype)
+            d_rotation = device.array(_rope_rotations(1, draft.config.head_size, draft.config.rope_theta,
+                                                      draft.dtype, offset=0))
+            d_bindings = dict(zip(d_nodes, [draft_token, d_rotation, d_attention, d_write, draft_pos,
+                                            *draft_caches]))
+            placement_host, write_host, attention_host = block_masks(len(prompt), width, context, self.dtype)
+            b_attention = device.array(attention_host)
+            b_placement = device.array(placement_host)
+            b_write = device.array(write_host)
+            b_pos = device.empty((), np.int32)
+            b_program, b_nodes = self._verifier(width, context, len(prompt), target_caches)
+            b_logits = device.empty(b_program._planned.output_nodes[0].shape, self.dtype)
+            b_rotation = device.array(_rope_rotations(width, self.config.head_size, self.config.rope_theta,
+                                                      self.dtype, offset=0))
+            b_bindings = dict(zip(b_nodes, [block_tokens, b_rotation, b_attention, b_placement, b_write, b_pos,
+                                            *target_caches]))
+            predictions = device.empty((width,), np.int32)
+            accepted = proposed = verifications = draft_calls = 0
+            lagging: Optional[int] = None
+            while len(generated) < max_new_tokens and not (stop_at_eos and token == eos):
+                limit = min(k, max_new_tokens - len(generated))
+                draft_position = len(draft_prompt) + len(generated) - 1
+                if lagging is not None:  # the draft consumes dk (its logits are not needed)
+                    device.upload(draft_token, np.array([[lagging]], np.int32))
+                    device.upload(draft_pos, np.asarray(draft_position - 1, np.int32))
+                    attention_host, write_host = decode_masks(draft_position - 1, draft_context, draft.dtype)
+                    device.upload(d_attention, attention_host)
+                    device.upload(d_write, write_host)
+                    d_program.run(d_bindings, out=[d_logits])
+                    draft_calls += 1
+                    lagging = None
+                device.upload(draft_token, np.array([[token]], np.int32))
+                device.upload(proposals, np.array([[token] + [0] * k], np.int32))
+                device.upload(draft_pos, np.asarray(draft_position, np.int32))
+                attention_host, write_host = decode_masks(draft_position, draft_context, draft.dtype)
+                device.upload(d_attention, attention_host)
+                device.upload(d_write, write_host)
+                for step in range(1, limit + 1):
+                    d_program.run(d_bindings, out=[d_logits])
+                    device.greedy_advance(d_logits, draft_token, history=proposals, step=step, position=draft_pos,
+                                          attention_mask=d_attention, write_mask=d_write,
+                                          cache_length=draft_context)
+                draft_calls += limit
+                position = len(prompt) + len(generated) - 1
+                rows = limit + 1 if bonus else limit
+                if rows != width:  # a short last round: its own block program
+                    block = device.to_numpy(proposals).reshape(-1)[:rows].tolist()
+                    preds, target_caches = self._verify_block(block, position, context, target_caches)
+                    proposal = device.to_numpy(proposals).reshape(-1)[1:limit + 1].tolist()
+                else:
+                    placement_host, write_host, attention_host = block_masks(position, width, context, self.dtype)
+                    device.upload(b_attention, attention_host)
+                    device.upload(b_placement, placement_host)
+                    device.upload(b_write, write_host)
+                    device.upload(b_pos, np.asarray(position, np.int32))
+                    b_program.run(b_bindings, out=[b_logits])
+                    device.greedy_advance(b_logits, predictions)
+                    preds = device.to_numpy(predictions).tolist()  # the round's one wait
+                    proposal = device.to_numpy(proposals).reshape(-1)[1:limit + 1].tolist()
+                if stop_at_eos and eos in proposal:
+                    proposal = proposal[: proposal.index(eos) + 1]
+                    preds = preds[: len(proposal) + (1 if bonus else 0)]
+                if bonus:
+                    decision = verify_greedy_block_with_bonus(proposal, preds)
+                    if decision.accepted_draft_tokens == len(proposal):
+                        lagging = proposal[-1]
+                else:
+                    decision = verify_greedy_candidates(proposal, preds)
+                emitted = list(decision.emitted_tokens)[: max_new_tokens - len(generated)]
+                if stop_at_eos and eos in emitted:
+                    emitted = emitted[: emitted.index(eos) + 1]
+                generated.extend(emitted)
+                token = emitted[-1]
+                accepted += decision.accepted_draft_tokens
+                proposed += len(proposal)
+                verifications += 1
+            device.synchronize()
+        decode_seconds = time.perf_counter() - decode_started
+        decode_tokens = len(generated) - 1
+        return {
+            "loop": "speculative-resident" + ("-bonus" if bonus else ""),
             "generated_token_ids": generated,
             "prompt_tokens": len(prompt),
             "generated_tokens": len(generated),

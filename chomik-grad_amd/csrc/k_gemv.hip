@@ -1285,14 +1285,52 @@ __global__ __launch_bounds__(exact_threads(VPL)) void k_gemv_exact(KArgs a) {
   using E = Elem<T>;
   using W = Word<T>;
   constexpr int V = 16 / sizeof(T);
-  extern __shared__ uint4 xs[];  // M x KV vectors of x
+  extern __shared__ uint4 xs[];  // M x KV vectors of x (normalised in place with the prologue)
   const int M = static_cast<int>(a.n[0]);
   const int64_t K = a.n[1];
   const int KV = static_cast<int>(K / V);
   const bool pro = a.n[5] == 1, silu = a.n[6] != 0, two = a.n[27] != 0;
   const int RG = silu ? 2 : 1;
   const int lane = threadIdx.x & 63;
+  const int waves = static_cast<int>(blockDim.x >> 6);
+  const int wave_in_block = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  // -- this wave's row group; its weight vectors are issued before x is
+  // staged (a wave past the last group reads the last group's rows and
+  // stores nothing)
+  const int64_t wave = blockIdx.x * int64_t(waves) + wave_in_block;
+  const Segments<T> st(a);
+  const int64_t groups = silu ? a.n[7] : st.total;
+  const bool active = wave < groups;
+  const int64_t gw = active ? wave : groups - 1;
+  const uint4* wrow[2];
+  int seg[2];
+  int64_t idx[2];
+  if (silu) {
+    wrow[0] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2]) + gw * K);
+    wrow[1] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[3]) + gw * K);
+    seg[0] = 0;
+    seg[1] = 1;
+    idx[0] = idx[1] = gw;
+  } else {
+    seg[0] = seg[1] = st.seg_of(gw);
+    idx[0] = idx[1] = gw - st.start(seg[0]);
+    wrow[0] = wrow[1] = reinterpret_cast<const uint4*>(st.weight(seg[0]) + idx[0] * K);
+  }
+  uint4 wv[2][VPL];
+  auto load_chunk = [&](int chunk) {
+    const int base = chunk * 64 * VPL + lane;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const int c = base + 64 * u;
+        wv[r][u] = (r < RG && (FULL || c < KV)) ? load_w<true>(wrow[r] + c) : zero;
+      }
+  };
+  if (FULL) load_chunk(0);
+  __builtin_amdgcn_sched_barrier(0);  // the weight stream before the staging
 
   {  // stage x (rows at stride n[2] elements, 16-byte aligned)
     const uint4* xg = static_cast<const uint4*>(a.p[0]);
@@ -1301,28 +1339,68 @@ __global__ __launch_bounds__(exact_threads(VPL)) void k_gemv_exact(KArgs a) {
   }
   __syncthreads();
 
-  const int64_t wave = blockIdx.x * int64_t(blockDim.x >> 6) +
-                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const Segments<T> st(a);
-  const int64_t groups = silu ? a.n[7] : st.total;
-  if (wave >= groups) return;  // no barrier below
-  const uint4* wrow[2];
-  int seg[2];
-  int64_t idx[2];
-  if (silu) {
-    wrow[0] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2]) + wave * K);
-    wrow[1] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[3]) + wave * K);
-    seg[0] = 0;
-    seg[1] = 1;
-    idx[0] = idx[1] = wave;
-  } else {
-    seg[0] = seg[1] = st.seg_of(wave);
-    idx[0] = idx[1] = wave - st.start(seg[0]);
-    wrow[0] = wrow[1] = reinterpret_cast<const uint4*>(st.weight(seg[0]) + idx[0] * K);
+  if (pro) {
+    // RMSNorm of row m by one wave, k_gemv_row's arithmetic on the same
+    // lane -> column map (one chunk covers K: the planner admits the
+    // prologue only then); the normalised words replace the row in LDS.
+    const uint4* ng = static_cast<const uint4*>(a.p[1]);
+    for (int m = wave_in_block; m < M; m += waves) {
+      uint32_t xw[VPL][4];
+      uint4 nv[VPL];
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const int c = lane + 64 * u;
+        const bool in = FULL || c < KV;
+        nv[u] = in ? load_x(ng + c) : zero;
+        const uint4 v = in ? xs[m * KV + c] : zero;
+        xw[u][0] = v.x;
+        xw[u][1] = v.y;
+        xw[u][2] = v.z;
+        xw[u][3] = v.w;
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int u = 0; u < VPL; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[u][i], xw[u][i]), W::kOnes, ss);
+      const float total = E::round(wave_sum(ss));
+      const float mean = E::round(total / E::round(static_cast<float>(K)));
+      const float rn = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+      const float inv = 1.0f / rn;
+      bool fast = W::fast_divisor(rn);
+      if constexpr (!W::kNoBranch) {
+#pragma unroll
+        for (int u = 0; u < VPL; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            fast = fast && W::fast_numerator(W::lo(xw[u][i])) && W::fast_numerator(W::hi(xw[u][i]));
+        fast = __all(fast);
+      }
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = W::lo(xw[u][i]), hi = W::hi(xw[u][i]);
+          float ql, qh;
+          if constexpr (W::kNoBranch) {
+            ql = fast ? quotient(lo, rn, inv) : lo * inv;
+            qh = fast ? quotient(hi, rn, inv) : hi * inv;
+          } else {
+            ql = fast ? quotient(lo, rn, inv) : lo / rn;
+            qh = fast ? quotient(hi, rn, inv) : hi / rn;
+          }
+          xw[u][i] = W::mul(W::pack(ql, qh), nw[i]);
+        }
+        const int c = lane + 64 * u;
+        if (FULL || c < KV) xs[m * KV + c] = make_uint4(xw[u][0], xw[u][1], xw[u][2], xw[u][3]);
+      }
+    }
+    __syncthreads();
   }
-  const uint4* ng = static_cast<const uint4*>(a.p[1]);
-  const int chunks = FULL ? 1 : (KV + 64 * VPL - 1) / (64 * VPL);
+  if (!active) return;  // no barrier below
 
+  const int chunks = FULL ? 1 : (KV + 64 * VPL - 1) / (64 * VPL);
   float acc[kMaxRows][2], acc2[kMaxRows][2];
 #pragma unroll
   for (int m = 0; m < kMaxRows; ++m)
@@ -1330,24 +1408,8 @@ __global__ __launch_bounds__(exact_threads(VPL)) void k_gemv_exact(KArgs a) {
     for (int r = 0; r < 2; ++r) acc[m][r] = acc2[m][r] = 0.f;
 
   for (int chunk = 0; chunk < chunks; ++chunk) {
+    if (!FULL) load_chunk(chunk);
     const int base = chunk * 64 * VPL + lane;
-    uint4 wv[2][VPL], nv[VPL];
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int u = 0; u < VPL; ++u) {
-        const int c = base + 64 * u;
-        if (r < RG && (FULL || c < KV)) {
-          wv[r][u] = load_w<true>(wrow[r] + c);
-        } else {
-          wv[r][u] = zero;
-        }
-      }
-#pragma unroll
-    for (int u = 0; u < VPL; ++u) {
-      const int c = base + 64 * u;
-      nv[u] = (pro && (FULL || c < KV)) ? load_x(ng + c) : zero;
-    }
     // m unrolled to constant indices (a runtime index would put acc in
     // private memory)
 #pragma unroll
@@ -1362,43 +1424,6 @@ __global__ __launch_bounds__(exact_threads(VPL)) void k_gemv_exact(KArgs a) {
         xw[u][1] = v.y;
         xw[u][2] = v.z;
         xw[u][3] = v.w;
-      }
-      if (pro) {  // one chunk covers K (the planner admits the prologue only then)
-        float ss = 0.f;
-#pragma unroll
-        for (int u = 0; u < VPL; ++u)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[u][i], xw[u][i]), W::kOnes, ss);
-        const float total = E::round(wave_sum(ss));
-        const float mean = E::round(total / E::round(static_cast<float>(K)));
-        const float rn = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
-        const float inv = 1.0f / rn;
-        bool fast = W::fast_divisor(rn);
-        if constexpr (!W::kNoBranch) {
-#pragma unroll
-          for (int u = 0; u < VPL; ++u)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              fast = fast && W::fast_numerator(W::lo(xw[u][i])) && W::fast_numerator(W::hi(xw[u][i]));
-          fast = __all(fast);
-        }
-#pragma unroll
-        for (int u = 0; u < VPL; ++u) {
-          const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float lo = W::lo(xw[u][i]), hi = W::hi(xw[u][i]);
-            float ql, qh;
-            if constexpr (W::kNoBranch) {
-              ql = fast ? quotient(lo, rn, inv) : lo * inv;
-              qh = fast ? quotient(hi, rn, inv) : hi * inv;
-            } else {
-              ql = fast ? quotient(lo, rn, inv) : lo / rn;
-              qh = fast ? quotient(hi, rn, inv) : hi / rn;
-            }
-            xw[u][i] = W::mul(W::pack(ql, qh), nw[i]);
-          }
-        }
       }
 #pragma unroll
       for (int r = 0; r < 2; ++r) {

@@ -57,9 +57,10 @@ def test_speculative_argument_checks():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("loop", ["reference", "resident"])
 @pytest.mark.parametrize("bonus", [False, True], ids=["reference-block", "bonus-block"])
-def test_speculative_on_hip_matches_oracle_and_greedy(hip, bonus):
-    print(f"[gpu case] speculative tiny bonus={bonus}", flush=True)
+def test_speculative_on_hip_matches_oracle_and_greedy(hip, bonus, loop):
+    print(f"[gpu case] speculative tiny bonus={bonus} loop={loop}", flush=True)
     target_cfg, target_w, draft_cfg, draft_w = tiny_pair()
     prompt = [5, 17, 3, 60, 2, 44]
     oracle = LlamaRuntime(target_cfg, target_w, compiler="cpu", dtype=np.float32).generate_speculative(
@@ -67,7 +68,8 @@ def test_speculative_on_hip_matches_oracle_and_greedy(hip, bonus):
         bonus=bonus)
     target = LlamaRuntime(target_cfg, target_w, compiler="hip", dtype=np.float32)
     draft = LlamaRuntime(draft_cfg, draft_w, compiler="hip", dtype=np.float32)
-    got = target.generate_speculative(draft, prompt, 12, speculative_tokens=3, bonus=bonus)
+    got = target.generate_speculative(draft, prompt, 12, speculative_tokens=3, bonus=bonus, loop=loop)
+    assert got["loop"].startswith("speculative-resident" if loop == "resident" else "speculative")
     assert got["generated_token_ids"] == oracle["generated_token_ids"]
     assert got["accepted_draft_tokens"] == oracle["accepted_draft_tokens"]
     assert got["generated_token_ids"] == target.generate(prompt, 12, loop="resident")["generated_token_ids"]
@@ -122,11 +124,12 @@ def test_c5_speculative_full_shape_equals_greedy(hip, tinyllama_runtime):
     draft = LlamaRuntime(draft_spec.config, synthetic.weights_as_tensors(
         synthetic.host_weights(draft_spec.config, draft_spec.dtype, seed=1)), compiler="hip", dtype=draft_spec.dtype)
     prompt = synthetic.prompt_ids(target.config.vocab_size, 256, seed=0).tolist()
-    result = target.generate_speculative(draft, prompt, 256, speculative_tokens=4, bonus=True)
-    assert result["generated_tokens"] == 256
     greedy = target.generate(prompt, 257, loop="resident")["generated_token_ids"][:256]
-    spec = result["generated_token_ids"]
-    first = next((i for i, (a, b) in enumerate(zip(spec, greedy)) if a != b), None)
-    assert first is None, f"speculative and greedy part at token {first}: {spec[first]} != {greedy[first]}"
-    print(f"C5: {result['warm_tokens_per_second']:.1f} tok/s, acceptance {result['acceptance_rate']:.3f}, "
-          f"{result['target_verification_calls']} verification blocks", flush=True)
+    for loop in ("resident", "reference"):
+        result = target.generate_speculative(draft, prompt, 256, speculative_tokens=4, bonus=True, loop=loop)
+        assert result["generated_tokens"] == 256
+        spec = result["generated_token_ids"]
+        first = next((i for i, (a, b) in enumerate(zip(spec, greedy)) if a != b), None)
+        assert first is None, f"{loop}: speculative and greedy part at token {first}: {spec[first]} != {greedy[first]}"
+        print(f"C5 {loop} loop: {result['warm_tokens_per_second']:.1f} tok/s, acceptance "
+              f"{result['acceptance_rate']:.3f}, {result['target_verification_calls']} verification blocks", flush=True)

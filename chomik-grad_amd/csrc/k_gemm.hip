@@ -36,6 +36,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int kBK = 64;            // k columns per LDS stage
 constexpr int kPad = 8;            // elements of padding per LDS row
 constexpr int kRow = kBK + kPad;   // LDS row length (elements)
+constexpr int kStages = 2;         // LDS stages of the straight-to-LDS kernel (4: one block per CU, slower)
 
 template <typename T> struct Mfma;
 template <> struct Mfma<__half> {
@@ -212,16 +213,192 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
     }
 }
 
+// 16 bytes per lane straight into LDS at lds + 16 * lane (a device function:
+// used directly in a kernel template body the builtin kept the host pass
+// from emitting the kernel's launch stub)
+__device__ __forceinline__ void lds_load16(const void* global, void* lds) {
+  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
+}
+
+// The same product with the operand tiles loaded straight into LDS
+// (global_load_lds_dwordx4: lane l of an instruction writes 16 bytes at the
+// wave's LDS base + 16 l, so one instruction fills 1 KiB contiguously, no
+// register staging and no bank conflict on the write).  A tile row is 8
+// chunks of 16 bytes with no padding; chunk c of row r is stored at
+// position c ^ ((r >> 1) & 7), so the 16 rows an MFMA fragment read touches
+// at one chunk fall in 16 distinct groups of 4 banks (rows of one parity
+// differ in the swizzle, the two parities in the half of the 128-byte row).
+// kStages stages of LDS keep kStages - 1 stages of loads in flight, one
+// barrier per stage; two stages (64 KiB at 128 x 128 tiles) leave room for
+// two blocks per CU, which measured faster than four stages at one block.  Out-of-range rows read a
+// clamped row (their results are not stored); K must be a multiple of the
+// 64-column stage.  Same arguments, epilogues and tile order as k_gemm_nt.
+template <typename T, int BM, int BN, bool SILU, bool RES>
+__global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
+  using E = Elem<T>;
+  constexpr int S = kStages;
+  constexpr int ON = SILU ? BN / 2 : BN;
+  constexpr int TM = BM / 2 / 16, TN = BN / 2 / 16;
+  constexpr int AI = BM * 8 / 256, WI = BN * 8 / 256;  // 1 KiB instructions per wave per stage
+  static_assert(AI >= 1 && WI >= 1, "tile too small for 256 threads");
+  __shared__ __attribute__((aligned(1024))) uint4 As[S][BM * 8];
+  __shared__ __attribute__((aligned(1024))) uint4 Ws[S][BN * 8];
+
+  const int64_t M = a.n[0], K = a.n[2];
+  const int64_t lda = a.n[4];
+  int64_t N = a.n[1], ldw = a.n[5], ldc = a.n[6];
+  const T* A = static_cast<const T*>(a.p[0]);
+  const T* W = static_cast<const T*>(a.p[1]);
+  T* C = static_cast<T*>(a.p[2]);
+  const T* R = static_cast<const T*>(a.p[3]);
+  const T* Wu = static_cast<const T*>(a.p[4]);
+  const int64_t ldr = a.n[7], ldwu = a.n[9];
+
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + ON - 1) / ON;
+  const int64_t tiles = tiles_m * tiles_n;
+  const int64_t per_xcd = (tiles + 7) / 8;
+  const int64_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (tile >= tiles) return;
+  const int64_t m0 = (tile / tiles_n) * BM;
+  int64_t n0 = (tile % tiles_n) * ON;
+  if (!SILU && !RES && a.n[11] > 1) {
+    const int64_t w0 = a.n[12], w1 = a.n[13], w2 = a.n[14];
+    const int seg = n0 < w0 ? 0 : n0 < w0 + w1 ? 1 : n0 < w0 + w1 + w2 ? 2 : 3;
+    n0 -= seg == 0 ? 0 : seg == 1 ? w0 : seg == 2 ? w0 + w1 : w0 + w1 + w2;
+    N = seg == 0 ? w0 : seg == 1 ? w1 : seg == 2 ? w2 : a.n[15];
+    ldc = seg == 0 ? a.n[16] : seg == 1 ? a.n[17] : seg == 2 ? a.n[18] : a.n[19];
+    ldw = seg == 0 ? a.n[20] : seg == 1 ? a.n[21] : seg == 2 ? a.n[22] : a.n[23];
+    W = static_cast<const T*>(seg == 0 ? a.p[1] : seg == 1 ? a.p[5] : seg == 2 ? a.p[7] : a.p[9]);
+    C = static_cast<T*>(seg == 0 ? a.p[2] : seg == 1 ? a.p[6] : seg == 2 ? a.p[8] : a.p[10]);
+  }
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fi = lane & 15, fg = lane >> 4;
+
+  // the source of each lane's vector: instruction j of this wave covers tile
+  // vectors v = (wave * I + j) * 64 + lane, row v / 8, stored chunk v % 8,
+  // global chunk stored ^ ((row >> 1) & 7); rows clamped into range
+  const T* asrc[AI];
+  const T* wsrc[WI];
+#pragma unroll
+  for (int j = 0; j < AI; ++j) {
+    const int v = (wave * AI + j) * 64 + lane, r = v >> 3, c = (v & 7) ^ ((r >> 1) & 7);
+    const int64_t m = m0 + r < M ? m0 + r : M - 1;
+    asrc[j] = A + m * lda + c * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < WI; ++j) {
+    const int v = (wave * WI + j) * 64 + lane, r = v >> 3, c = (v & 7) ^ ((r >> 1) & 7);
+    if (SILU) {
+      const int f = r >> 4;
+      int64_t n = n0 + 16 * (f >> 1) + (r & 15);
+      n = n < N ? n : N - 1;
+      wsrc[j] = ((f & 1) ? Wu + n * ldwu : W + n * ldw) + c * 8;
+    } else {
+      const int64_t n = n0 + r < N ? n0 + r : N - 1;
+      wsrc[j] = W + n * ldw + c * 8;
+    }
+  }
+  auto load_stage = [&](int64_t k0, int b) {
+#pragma unroll
+    for (int j = 0; j < AI; ++j) lds_load16(asrc[j] + k0, &As[b][(wave * AI + j) * 64]);
+#pragma unroll
+    for (int j = 0; j < WI; ++j) lds_load16(wsrc[j] + k0, &Ws[b][(wave * WI + j) * 64]);
+  };
+
+  f4v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+
+  // stage k + S - 1 is issued while stage k is multiplied; after the barrier
+  // at the top of iteration k every wave has finished stage k - 1, whose
+  // buffer that issue reuses
+  const int nst = static_cast<int>(K / kBK);
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nst) load_stage(int64_t(st) * kBK, st);
+  for (int k = 0; k < nst; ++k) {
+    // stage k has landed once at most min(S - 2, nst - 1 - k) later stages
+    // of this wave are outstanding (the barrier covers the other waves)
+    const int later = nst - 1 - k < S - 2 ? nst - 1 - k : S - 2;
+    if (later >= 2) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * (AI + WI)) : "memory");
+    else if (later == 1) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AI + WI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (k + S - 1 < nst) load_stage(int64_t(k + S - 1) * kBK, (k + S - 1) % S);
+    const int buf = k % S;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      uint4 fa[TM], fw[TN];
+      const int c = ks * 4 + fg;  // logical chunk of this lane's eight k values
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * (BM / 2) + i * 16 + fi;
+        fa[i] = As[buf][r * 8 + (c ^ ((r >> 1) & 7))];
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * (BN / 2) + j * 16 + fi;
+        fw[j] = Ws[buf][r * 8 + (c ^ ((r >> 1) & 7))];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::step(fa[i], fw[j], acc[i][j]);
+    }
+  }
+
+  if (SILU) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; j += 2) {
+        const int64_t n = n0 + 16 * ((wn * TN + j) >> 1) + fi;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = m0 + wm * (BM / 2) + i * 16 + fg * 4 + r;
+          const float g = E::round(acc[i][j][r]);
+          const float u = E::round(acc[i][j + 1][r]);
+          const float denom = E::round(E::round(expf(-g)) + 1.f);
+          if (m < M && n < N) C[m * ldc + n] = E::from_f(E::round(E::round(g / denom) * u));
+        }
+      }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t n = n0 + wn * (BN / 2) + j * 16 + fi;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * (BM / 2) + i * 16 + fg * 4 + r;
+        if (m < M && n < N) {
+          float y = E::round(acc[i][j][r]);
+          if (RES) y = E::round(E::to_f(R[m * ldr + n]) + y);
+          C[m * ldc + n] = E::from_f(y);
+        }
+      }
+    }
+}
+
 template <typename T, bool SILU, bool RES>
-const void* pick_gemm_tile(bool big) {
+const void* pick_gemm_tile(bool big, bool lds) {
+  if (lds)
+    return big ? reinterpret_cast<const void*>(&k_gemm_lds<T, 128, 128, SILU, RES>)
+               : reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES>);
   return big ? reinterpret_cast<const void*>(&k_gemm_nt<T, 128, 128, SILU, RES>)
              : reinterpret_cast<const void*>(&k_gemm_nt<T, 64, 64, SILU, RES>);
 }
 
 template <typename T>
-const void* pick_gemm(bool big, bool silu, bool res) {
-  if (silu) return pick_gemm_tile<T, true, false>(big);
-  return res ? pick_gemm_tile<T, false, true>(big) : pick_gemm_tile<T, false, false>(big);
+const void* pick_gemm(bool big, bool silu, bool res, bool lds) {
+  if (silu) return pick_gemm_tile<T, true, false>(big, lds);
+  return res ? pick_gemm_tile<T, false, true>(big, lds) : pick_gemm_tile<T, false, false>(big, lds);
 }
 
 const char* plan_gemm(KArgs& a, Launch& l) {
@@ -261,7 +438,14 @@ const char* plan_gemm(KArgs& a, Launch& l) {
   const int64_t tiles = ((M + bm - 1) / bm) * ((N + on - 1) / on);
   const int64_t blocks = 8 * ((tiles + 7) / 8);
   if (blocks > 2147483647) return "gemm: too many tiles";
-  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res) : pick_gemm<bf16_t>(big, silu, res);
+  // straight-to-LDS tiles when K is a whole number of 64-column stages
+  // (CHOMIK_HIP_GEMM_LDS=0 keeps the register-staged kernel)
+  static const int lds_knob = [] {
+    const char* v = std::getenv("CHOMIK_HIP_GEMM_LDS");
+    return v && *v ? std::atoi(v) : 1;
+  }();
+  const bool lds = lds_knob != 0 && K % kBK == 0;
+  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res, lds) : pick_gemm<bf16_t>(big, silu, res, lds);
   l.grid = dim3(static_cast<unsigned>(blocks));
   l.block = dim3(256);
   l.shmem = 0;

@@ -302,7 +302,7 @@ def c4_measurement(device, lib, steps: int, warmup: int) -> dict:
     }
 
 
-def c5_measurement(target, tokens: int) -> dict:
+def c5_measurement(target, tokens: int, lib=None) -> dict:
     """C5: the 2-layer dim-512 fp16 draft (seed 1) proposing k = 4 greedy
     tokens per round for the C2 target, verified in 5-token blocks; 256-token
     random prompt.  Timed on the second (warm) run."""
@@ -315,9 +315,17 @@ def c5_measurement(target, tokens: int) -> dict:
     prompt = synthetic.prompt_ids(target.config.vocab_size, 256, seed=0).tolist()
     target.generate_speculative(draft, prompt, tokens, speculative_tokens=4, bonus=True)
     result = target.generate_speculative(draft, prompt, tokens, speculative_tokens=4, bonus=True)
+    block = {}
+    if lib is not None:
+        # the 5-row verification block: each kernel group's average duration
+        programs = [entry[0] for key, entry in target._block_programs.items() if key[0] == 5]
+        if programs:
+            block = plan_breakdown(programs[0], lib, rounds=10)
     return {
         "workload": "C5: greedy speculative decoding, 2-layer dim-512 draft (k = 4) for the C2 target, "
                     "5-token verification blocks, 256-token prompt",
+        "verify_block_kernels": block,
+        "verify_block_kernel_ms": round(sum(v["total_ms"] for v in block.values()), 3) if block else None,
         "generated_tokens": result["generated_tokens"],
         "tok_per_s": round(result["warm_tokens_per_second"], 1),
         "acceptance_rate": round(result["acceptance_rate"], 4),
@@ -523,7 +531,7 @@ def main() -> int:
     c5 = None
     if args.c5_tokens:
         log(f"C5 speculative decoding of {args.c5_tokens} tokens")
-        c5 = c5_measurement(runtime, args.c5_tokens)
+        c5 = c5_measurement(runtime, args.c5_tokens, lib)
         log(f"C5: {c5['tok_per_s']} tok/s, acceptance {c5['acceptance_rate']}")
     c4 = None
     if args.c4_steps:

@@ -284,6 +284,15 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// 16 bytes per lane straight into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4; lds is the wave-uniform base, so one instruction
+// fills 1 KiB contiguously).  A device function: used directly in a kernel
+// template body the builtin kept the host pass from emitting the kernel's
+// launch stub.
+__device__ __forceinline__ void lds_load16(const void* global, void* lds) {
+  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
+}
+
 // Sum over a 256-thread block (4 waves); every thread gets the result.
 __device__ __forceinline__ float block_sum256(float v, float* scratch4) {
   v = wave_sum(v);

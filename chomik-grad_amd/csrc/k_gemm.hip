@@ -213,13 +213,6 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
     }
 }
 
-// 16 bytes per lane straight into LDS at lds + 16 * lane (a device function:
-// used directly in a kernel template body the builtin kept the host pass
-// from emitting the kernel's launch stub)
-__device__ __forceinline__ void lds_load16(const void* global, void* lds) {
-  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
-}
-
 // The same product with the operand tiles loaded straight into LDS
 // (global_load_lds_dwordx4: lane l of an instruction writes 16 bytes at the
 // wave's LDS base + 16 l, so one instruction fills 1 KiB contiguously, no

@@ -40,6 +40,7 @@ constexpr int kMaxRows = 8;
 template <typename T>
 struct Segments {
   int64_t e0, e1, e2, total;  // cumulative row ends (INT64_MAX past the last segment)
+  int i0, i1, i2;             // the same clamped to 32 bits (for seg_of32)
   const T* w[4];
   T* out[4];
   const T* res[4];
@@ -57,6 +58,10 @@ struct Segments {
     e1 = segs > 2 ? c1 : big;
     e2 = segs > 3 ? c2 : big;
     total = segs == 1 ? c0 : segs == 2 ? c1 : segs == 3 ? c2 : c3;
+    const int64_t cap = 2147483647;
+    i0 = static_cast<int>(e0 < cap ? e0 : cap);
+    i1 = static_cast<int>(e1 < cap ? e1 : cap);
+    i2 = static_cast<int>(e2 < cap ? e2 : cap);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       w[i] = static_cast<const T*>(a.p[2 + i]);
@@ -67,6 +72,8 @@ struct Segments {
     }
   }
   __device__ int seg_of(int64_t g) const { return (g >= e0) + (g >= e1) + (g >= e2); }
+  // rows below 2^31: scalar compares (a 64-bit compare goes through a VGPR)
+  __device__ int seg_of32(int g) const { return (g >= i0) + (g >= i1) + (g >= i2); }
   __device__ int64_t start(int s) const { return pick(s, int64_t(0), e0, e1, e2); }
   __device__ const T* weight(int s) const { return pick(s, w[0], w[1], w[2], w[3]); }
   __device__ T* output(int s) const { return pick(s, out[0], out[1], out[2], out[3]); }
@@ -711,13 +718,13 @@ __global__ __launch_bounds__(256) void k_gemv_stream(KArgs a) {
 
   const Segments<T> st(a);
   // weight row r of group g: its segment and the row within it
-  auto locate = [&](int64_t g, int r, int& seg, int64_t& idx) -> const uint4* {
+  auto locate = [&](int g, int r, int& seg, int64_t& idx) -> const uint4* {
     if (SILU) {
       seg = r;
       idx = g;
       return reinterpret_cast<const uint4*>((r == 0 ? st.w[0] : st.w[1]) + g * K);
     }
-    seg = st.seg_of(g);
+    seg = st.seg_of32(g);
     idx = g - st.start(seg);
     return reinterpret_cast<const uint4*>(st.weight(seg) + idx * K);
   };
@@ -742,7 +749,7 @@ __global__ __launch_bounds__(256) void k_gemv_stream(KArgs a) {
     int64_t idx;
     float res;
   };
-  auto issue = [&](Group& b, int64_t g) {
+  auto issue = [&](Group& b, int g) {
     const uint4* wp[RG];
     int sg[RG];
     int64_t ix[RG];
@@ -757,7 +764,7 @@ __global__ __launch_bounds__(256) void k_gemv_stream(KArgs a) {
       for (int u = 0; u < VPL; ++u) b.w[r][u] = load_w<NT>(wp[r] + lane + 64 * u);
   };
   Group A, B;
-  issue(A, g0);
+  issue(A, static_cast<int>(g0));
   __builtin_amdgcn_sched_barrier(0);  // the first rows stream during the prologue
 
   uint32_t xw[VPL][4];
@@ -834,11 +841,15 @@ __global__ __launch_bounds__(256) void k_gemv_stream(KArgs a) {
       }
     }
   };
-  for (int64_t g = g0; g < g1; g += 2) {
-    issue(B, g + 1 < g1 ? g + 1 : g);
+  // 32-bit group indices (row counts stay far below 2^31): scalar compares;
+  // 64-bit ones went through a VGPR whose write waited for every load in
+  // flight at the top of each iteration
+  const int e0 = static_cast<int>(g0), e1 = static_cast<int>(g1);
+  for (int g = e0; g < e1; g += 2) {
+    issue(B, g + 1 < e1 ? g + 1 : g);
     finish(A);
-    if (g + 1 >= g1) break;
-    issue(A, g + 2 < g1 ? g + 2 : g + 1);
+    if (g + 1 >= e1) break;
+    issue(A, g + 2 < e1 ? g + 2 : g + 1);
     finish(B);
   }
 }
@@ -1473,6 +1484,234 @@ __global__ __launch_bounds__(exact_threads(VPL)) void k_gemv_exact(KArgs a) {
   }
 }
 
+// Streaming form of k_gemv_exact for exact fits (K / 8 == 64 VPL), with the
+// same per-row arithmetic.  n[23] waves each own a contiguous run of row
+// groups and walk it with the next group's weight rows and residuals in
+// flight while the current group's M rows are reduced, so the M-fold
+// arithmetic overlaps the weight stream instead of following it.  The x rows
+// (and the RMSNorm weight) are loaded before the weights and written to LDS,
+// so waiting for them never waits for the weight stream (a global_load_lds
+// transfer would: the compiler then drains every load before each LDS read);
+// they are normalised once per block (wave m of the block takes rows m,
+// m + 4, ...).  LDS: M rows of x, then the norm weight row.
+template <typename T, int VPL, bool SILU>
+__global__ __launch_bounds__(256) void k_gemv_exact_run(KArgs a) {
+  using E = Elem<T>;
+  using W = Word<T>;
+  constexpr int V = 16 / sizeof(T);
+  constexpr int KV = 64 * VPL;      // 16-byte vectors per row
+  constexpr int RG = SILU ? 2 : 1;  // weight rows per group
+  constexpr int WAVES = 4;
+  extern __shared__ uint4 xs[];
+  const int M = static_cast<int>(a.n[0]);
+  const int64_t K = a.n[1];
+  const bool pro = a.n[5] == 1, two = a.n[27] != 0;
+  const int lane = threadIdx.x & 63;
+  const int wave_in_block = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t wave = blockIdx.x * int64_t(WAVES) + wave_in_block;
+  const int64_t nwaves = a.n[23];
+  const Segments<T> st(a);
+  const int64_t groups = SILU ? a.n[7] : st.total;
+  const int64_t g0 = wave < nwaves ? wave * groups / nwaves : groups;
+  const int64_t g1 = wave < nwaves ? (wave + 1) * groups / nwaves : groups;
+  const bool active = g0 < g1;
+
+  // -- x rows and the norm weight: piece j (row j / VPL, vectors
+  // 64 (j % VPL) + lane) is wave j % 4's; a fixed count per wave, indices
+  // past the last piece clamped to it (a repeated, identical copy), so every
+  // load is unconditional
+  constexpr int kPieces = (kMaxRows + 1) * VPL;
+  constexpr int kPerWave = (kPieces + WAVES - 1) / WAVES;
+  const int pieces = (M + (pro ? 1 : 0)) * VPL;
+  uint4 xv[kPerWave];
+  int xdst[kPerWave];
+  {
+    const T* xg = static_cast<const T*>(a.p[0]);
+    const int64_t xstride = a.n[2];
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      int j = wave_in_block + WAVES * q;
+      j = j < pieces ? j : pieces - 1;
+      const int m = j / VPL, u = j % VPL;
+      const T* src = m < M ? xg + m * xstride : static_cast<const T*>(a.p[1]);
+      xv[q] = load_x(reinterpret_cast<const uint4*>(src) + 64 * u + lane);
+      xdst[q] = m * KV + 64 * u + lane;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  struct Group {
+    uint4 w[RG][VPL];
+    int seg;
+    int64_t idx;
+    float res[kMaxRows];
+  };
+  // Every load is unconditional (a row past M, or a segment without a
+  // residual, reads x[0] and discards it) so the wait counts stay exact.
+  auto issue = [&](Group& b, int g) {
+    const uint4* wp[RG];
+    if (SILU) {
+      b.seg = 0;
+      b.idx = g;
+      wp[0] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[2]) + g * K);
+      wp[RG - 1] = reinterpret_cast<const uint4*>(static_cast<const T*>(a.p[3]) + g * K);
+    } else {
+      b.seg = st.seg_of32(g);
+      b.idx = g - st.start(b.seg);
+      wp[0] = reinterpret_cast<const uint4*>(st.weight(b.seg) + b.idx * K);
+      const T* r = st.residual(b.seg);
+      const int64_t rs = st.res_stride(b.seg);
+#pragma unroll
+      for (int m = 0; m < kMaxRows; ++m) {
+        const T* src = (r && m < M) ? r + m * rs + b.idx : static_cast<const T*>(a.p[0]);
+        b.res[m] = E::to_f(*src);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) b.w[r][u] = load_w<true>(wp[r] + lane + 64 * u);
+  };
+  Group A, B;
+  issue(A, static_cast<int>(active ? g0 : groups - 1));
+  // x into LDS (the stores wait for the x loads only); then every wave's
+  // stores are complete (lgkmcnt) at the barrier.  Wait and barrier are one
+  // asm statement, a compiler memory barrier as well: __syncthreads' fence
+  // would drain every load in flight, group A's weights included.
+#pragma unroll
+  for (int q = 0; q < kPerWave; ++q) xs[xdst[q]] = xv[q];
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  if (pro) {
+    // RMSNorm of row m, k_gemv_row's arithmetic on the same lane -> column
+    // map; the normalised words replace the row in LDS
+    for (int m = wave_in_block; m < M; m += WAVES) {
+      uint32_t xw[VPL][4];
+      uint4 nv[VPL];
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        nv[u] = xs[M * KV + lane + 64 * u];
+        const uint4 v = xs[m * KV + lane + 64 * u];
+        xw[u][0] = v.x;
+        xw[u][1] = v.y;
+        xw[u][2] = v.z;
+        xw[u][3] = v.w;
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int u = 0; u < VPL; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[u][i], xw[u][i]), W::kOnes, ss);
+      const float total = E::round(wave_sum(ss));
+      const float mean = E::round(total / E::round(static_cast<float>(K)));
+      const float rn = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+      const float inv = 1.0f / rn;
+      bool fast = W::fast_divisor(rn);
+      if constexpr (!W::kNoBranch) {
+#pragma unroll
+        for (int u = 0; u < VPL; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            fast = fast && W::fast_numerator(W::lo(xw[u][i])) && W::fast_numerator(W::hi(xw[u][i]));
+        fast = __all(fast);
+      }
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const uint32_t nw[4] = {nv[u].x, nv[u].y, nv[u].z, nv[u].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = W::lo(xw[u][i]), hi = W::hi(xw[u][i]);
+          float ql, qh;
+          if constexpr (W::kNoBranch) {
+            ql = fast ? quotient(lo, rn, inv) : lo * inv;
+            qh = fast ? quotient(hi, rn, inv) : hi * inv;
+          } else {
+            ql = fast ? quotient(lo, rn, inv) : lo / rn;
+            qh = fast ? quotient(hi, rn, inv) : hi / rn;
+          }
+          xw[u][i] = W::mul(W::pack(ql, qh), nw[i]);
+        }
+        xs[m * KV + lane + 64 * u] = make_uint4(xw[u][0], xw[u][1], xw[u][2], xw[u][3]);
+      }
+    }
+    // the normalised rows are in LDS (lgkmcnt) for every wave; the weight
+    // loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+  if (!active) return;  // no barrier below
+
+  // the M rows of one group: per row and weight row, k_gemv_row's one chain
+  // in (u, i) order or k_gemv_stream's two chains, then the wave sum and the
+  // epilogue.  (Computing all kMaxRows slots as straight-line code so the
+  // rows' chains interleave measured slower: the kernel is bound by its
+  // VALU work, which that adds to.)
+  auto finish = [&](const Group& b) {
+    float y[kMaxRows][RG];
+#pragma unroll
+    for (int m = 0; m < kMaxRows; ++m) {
+      if (m >= M) break;
+      uint32_t xw[VPL][4];
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        const uint4 v = xs[m * KV + lane + 64 * u];
+        xw[u][0] = v.x;
+        xw[u][1] = v.y;
+        xw[u][2] = v.z;
+        xw[u][3] = v.w;
+      }
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        float s0 = 0.f, s1 = 0.f;
+        if (two) {
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) {
+            const uint32_t ww[4] = {b.w[r][u].x, b.w[r][u].y, b.w[r][u].z, b.w[r][u].w};
+            s0 = W::dot(xw[u][0], ww[0], s0);
+            s1 = W::dot(xw[u][1], ww[1], s1);
+            s0 = W::dot(xw[u][2], ww[2], s0);
+            s1 = W::dot(xw[u][3], ww[3], s1);
+          }
+          y[m][r] = wave_sum(s0 + s1);
+        } else {
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) {
+            const uint32_t ww[4] = {b.w[r][u].x, b.w[r][u].y, b.w[r][u].z, b.w[r][u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s0 = W::dot(xw[u][i], ww[i], s0);
+          }
+          y[m][r] = wave_sum(s0);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxRows; ++m) {
+      if (m >= M) break;
+      if (SILU) {
+        const float g = E::round(y[m][0]);
+        const float u = E::round(y[m][RG - 1]);
+        const float denom = E::round(E::round(expf(-g)) + 1.f);
+        const T out = E::from_f(E::round(E::round(g / denom) * u));
+        if (lane == 0) static_cast<T*>(a.p[6])[m * a.n[11] + b.idx] = out;
+      } else {
+        float v = E::round(y[m][0]);
+        if (st.residual(b.seg)) v = E::round(b.res[m] + v);
+        if (lane == 0) st.output(b.seg)[m * st.out_stride(b.seg) + b.idx] = E::from_f(v);
+      }
+    }
+  };
+  // 32-bit group indices (row counts stay far below 2^31): scalar compares;
+  // 64-bit ones went through a VGPR whose write waited for every load in
+  // flight at the top of each iteration
+  const int e0 = static_cast<int>(g0), e1 = static_cast<int>(g1);
+  for (int g = e0; g < e1; g += 2) {
+    issue(B, g + 1 < e1 ? g + 1 : g);
+    finish(A);
+    if (g + 1 >= e1) break;
+    issue(A, g + 2 < e1 ? g + 2 : g + 1);
+    finish(B);
+  }
+}
+
 // The (VPL, FULL) the M = 1 kernel of this matrix uses: k_gemv_stream's exact
 // fits (pick_stream) with two chains, else k_gemv_row's (pick_row_nt).
 template <typename T>
@@ -1496,6 +1735,26 @@ const void* pick_exact(int64_t kv, bool pro, bool silu, bool two) {
 }
 
 constexpr size_t kExactStageBytes = 64 * 1024;
+
+// k_gemv_exact_run for the exact fits (the widths k_gemv_row / k_gemv_stream
+// serve unmasked), nullptr otherwise.
+template <typename T>
+const void* pick_exact_run(int64_t kv, bool pro, bool silu) {
+  if (kv % 64) return nullptr;
+  switch (kv / 64) {
+    case 1: return silu ? reinterpret_cast<const void*>(&k_gemv_exact_run<T, 1, true>)
+                        : reinterpret_cast<const void*>(&k_gemv_exact_run<T, 1, false>);
+    case 2: return silu ? reinterpret_cast<const void*>(&k_gemv_exact_run<T, 2, true>)
+                        : reinterpret_cast<const void*>(&k_gemv_exact_run<T, 2, false>);
+    case 4: return silu ? reinterpret_cast<const void*>(&k_gemv_exact_run<T, 4, true>)
+                        : reinterpret_cast<const void*>(&k_gemv_exact_run<T, 4, false>);
+    case 8: return silu ? reinterpret_cast<const void*>(&k_gemv_exact_run<T, 8, true>)
+                        : reinterpret_cast<const void*>(&k_gemv_exact_run<T, 8, false>);
+    case 11: return silu ? nullptr : reinterpret_cast<const void*>(&k_gemv_exact_run<T, 11, false>);
+    case 16: return (silu || pro) ? nullptr : reinterpret_cast<const void*>(&k_gemv_exact_run<T, 16, false>);
+    default: return nullptr;
+  }
+}
 
 const char* plan_gemv(KArgs& a, Launch& l) {
   const int64_t M = a.n[0], K = a.n[1];
@@ -1547,10 +1806,28 @@ const char* plan_gemv(KArgs& a, Launch& l) {
   if (a.n[26] != 0 && M >= 2 && (dt == F16 || dt == BF16) && aligned &&
       (!pro || (a.n[19] == dt && one_pass)) && exact_bytes <= kExactStageBytes) {
     const int64_t groups = silu ? a.n[7] : rows;
+    a.n[27] = stream_pick ? 1 : 0;
+    // Large exact fits: the streaming form over contiguous runs of row groups
+    // (measured on the verification block of five rows: gate/up, 5632
+    // groups, 18.5 -> 15.7 us at 2048 waves; the 32000-row lm_head 48.6 ->
+    // 31.2 us at 4096; below 4096 groups one group per wave was faster).
+    // CHOMIK_HIP_GEMV_EXACT_WAVES fixes the wave count (0: never stream).
+    static const int exact_waves = env_int("CHOMIK_HIP_GEMV_EXACT_WAVES", -1);
+    const size_t run_bytes = static_cast<size_t>((M + (pro ? 1 : 0)) * K) * dtype_size(dt);
+    const void* run = dt == F16 ? pick_exact_run<__half>(kv, pro, silu) : pick_exact_run<bf16_t>(kv, pro, silu);
+    const int64_t want = exact_waves >= 0 ? exact_waves : groups < 4096 ? 0 : groups < 16384 ? 2048 : 4096;
+    if (run && run_bytes <= kExactStageBytes && want >= 1) {
+      const int64_t nwaves = groups < want ? groups : want;
+      a.n[23] = nwaves;
+      l.func = run;
+      l.grid = dim3(static_cast<unsigned>((nwaves + 3) / 4));
+      l.block = dim3(256);
+      l.shmem = run_bytes;
+      return nullptr;
+    }
     const int threads = exact_threads(static_cast<int>(kv % 64 == 0 ? kv / 64 : 4));
     const int64_t blocks = (groups + threads / 64 - 1) / (threads / 64);
     if (blocks > 2147483647) return "gemv: too many rows";
-    a.n[27] = stream_pick ? 1 : 0;
     l.func = dt == F16 ? pick_exact<__half>(kv, pro, silu, stream_pick)
                        : pick_exact<bf16_t>(kv, pro, silu, stream_pick);
     if (!l.func) return "gemv: no row-exact kernel for this width";

@@ -60,6 +60,14 @@ def test_c4_shapes_match_oracle(hip):
     gpu_error = np.abs(got_logits - truth).mean()
     oracle_error = np.abs(want_logits - truth).mean()
     print(f"mean |logit error| vs float32: hip {gpu_error:.5f}, bf16 oracle {oracle_error:.5f}", flush=True)
+    # The tolerance measured against float32 itself: the bfloat16 oracle misses
+    # it for a comparable share of logits, so no bfloat16 evaluation can be
+    # held to it on every logit.
+    def share_outside(values):
+        return float((np.abs(values - truth) > ATOL + RTOL * np.abs(truth)).mean())
+    print(f"share outside atol {ATOL}/rtol {RTOL}: hip vs oracle {outside.mean():.5f}, "
+          f"hip vs float32 {share_outside(got_logits):.5f}, oracle vs float32 {share_outside(want_logits):.5f}; "
+          f"max |hip - oracle| {np.abs(got_logits - want_logits).max():.4f}", flush=True)
     assert gpu_error <= oracle_error * 1.05
 
 

@@ -1317,6 +1317,61 @@ def fuse_block_attention(steps: List[Step], outputs: List[PV], emitter: "Emitter
     return [s for s in steps if id(s) not in removed]
 
 
+def _same_view(a: PV, b: PV) -> bool:
+    return (a.storage is b.storage and a.offset == b.offset and tuple(a.shape) == tuple(b.shape)
+            and tuple(a.strides) == tuple(b.strides) and a.dtype == b.dtype)
+
+
+def fuse_block_kv_place(steps: List[Step], outputs: List[PV]) -> List[Step]:
+    """A layer's key and value placement (two kv_place steps with the same
+    placement, write mask and cache geometry, the keys coming from a rope
+    step read by nothing else) -> one paired kv_place step that rotates the
+    keys on load: a verification block's three launches per layer become
+    one.  The fused step takes the later placement's place in the order, and
+    only if nothing in between reads the earlier one's cache."""
+    counts = _consumers(steps, outputs)
+    producer = _producer(steps)
+    removed: Set[int] = set()
+    places = [(i, st) for i, st in enumerate(steps) if st.kind == K_KV_PLACE]
+    for index, pk in places:
+        if id(pk) in removed or pk.attrs.get("pair"):
+            continue
+        cache, x, placement, w = pk.ins
+        found = producer.get(id(x.storage))
+        if found is None:
+            continue
+        rope = found[1]
+        if (rope.kind != K_ROPE or rope.attrs["mode"] not in (0, 1) or counts.get(id(x.storage)) != 1
+                or not x.whole() or x.shape != rope.ins[0].shape or cache.shape[3] % 2):
+            continue
+        for jndex, pv in places:
+            if pv is pk or id(pv) in removed or pv.attrs.get("pair"):
+                continue
+            cache_v, xv, placement_v, w_v = pv.ins
+            rope_v = producer.get(id(xv.storage))
+            if rope_v is not None and rope_v[1].kind == K_ROPE:
+                continue
+            if not (_same_view(placement_v, placement) and _same_view(w_v, w)
+                    and pv.attrs["in_place"] == pk.attrs["in_place"] and cache_v.shape == cache.shape
+                    and cache_v.strides == cache.strides and cache_v.dtype == cache.dtype
+                    and xv.shape == x.shape and xv.dtype == x.dtype):
+                continue
+            first, last = sorted((index, jndex))
+            early = steps[first]
+            between = steps[first + 1:last]
+            if any(pv2.storage is early.outs[0].storage or pv2.storage is early.ins[0].storage
+                   for st in between for pv2 in st.reads()):
+                continue
+            fused = Step(K_KV_PLACE, [cache, rope.ins[0], placement, w, cache_v, xv, rope.ins[2], rope.ins[1]],
+                         [pk.outs[0], pv.outs[0]],
+                         dict(pk.attrs, pair=True, rope={"mode": rope.attrs["mode"], "offset": rope.attrs["offset"],
+                                                         "table_length": rope.attrs["table_length"]}))
+            steps[last] = fused
+            removed.update({id(early), id(rope)})
+            break
+    return [st for st in steps if id(st) not in removed]
+
+
 def fuse_attention_projection(steps: List[Step], outputs: List[PV]) -> List[Step]:
     """Batch-1 chunk decode attention whose output feeds only the next
     single-row GEMV (the o projection, residual epilogue or none) -> the
@@ -1598,7 +1653,7 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         ints += list(cache.strides) + [dtype_code(w.dtype)]
         return kind, [_ptr(cache), _ptr(x), _ptr(w), _ptr(out)], ints, []
     if kind == K_KV_PLACE:
-        cache, x, placement, w = step.ins
+        cache, x, placement, w = step.ins[:4]
         out = step.outs[0]
         b, kv, c, hd = cache.shape
         t = x.shape[2]
@@ -1607,7 +1662,16 @@ def encode(step: Step) -> Tuple[int, List[Tuple[int, int]], List[int], List[floa
         ints = [b, kv, c, hd, dtype_code(cache.dtype), t] + xs + list(placement.strides)
         ints += [ws[0], ws[2], 1 if a["in_place"] else 0] + list(cache.strides)
         ints += [dtype_code(placement.dtype), dtype_code(w.dtype)]
-        return kind, [_ptr(cache), _ptr(x), _ptr(placement), _ptr(w), _ptr(out)], ints, []
+        ptrs = [_ptr(cache), _ptr(x), _ptr(placement), _ptr(w), _ptr(out)]
+        if a.get("pair"):
+            # the value placement (p[5..7]) and the keys' RoPE (table p[8],
+            # position p[9])
+            cache_v, xv, table, position = step.ins[4:8]
+            ints += [1] + broadcast_strides(xv, (b, kv, t, hd))
+            r = a["rope"]
+            ints += [1, 1 if r["mode"] == 1 else 0, r["offset"], r["table_length"]]
+            ptrs += [_ptr(cache_v), _ptr(xv), _ptr(step.outs[1]), _ptr(table), _ptr(position)]
+        return kind, ptrs, ints, []
     if kind == K_DECODE_ATTN and a.get("read_only"):
         # T query rows of one block as T sequences over one cache (batch
         # stride 0): q strides (t, h, d), mask strides (t, h, c)
@@ -1748,6 +1812,8 @@ def describe(step: Step, names: Dict[int, str]) -> str:
         label = "fused_elementwise" if len(a["ops"]) > 1 else f"elementwise_{a['expression'][0]}"
     if step.kind == K_DECODE_ATTN and a.get("read_only"):
         label = "decode_attention[block]"
+    if step.kind == K_KV_PLACE and a.get("pair"):
+        label = "kv_place[rope+pair]"
     ins = ", ".join(name(pv) for pv in step.ins)
     outs = ", ".join(name(pv) for pv in step.outs)
     shape = tuple(step.outs[0].shape) if step.outs else ()
@@ -1776,6 +1842,7 @@ def plan_graph(compiler, outputs: Sequence[LazyNode], dynamic_inputs: Sequence[L
     steps = merge_sibling_gemms(steps)
     steps = fuse_decode_attention(steps, out_pvs, emitter)
     steps = fuse_block_attention(steps, out_pvs, emitter)
+    steps = fuse_block_kv_place(steps, out_pvs)
     steps = fuse_attention_projection(steps, out_pvs)
     steps = attach_gemv_workspace(steps, emitter)
 

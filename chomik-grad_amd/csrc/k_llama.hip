@@ -371,11 +371,28 @@ const char* plan_kv_write(KArgs& a, Launch& l) {
 // (b, kv, t, d), n[10..11] placement strides (t, row), n[12..13] w strides
 // (b, row), n[14] in place, n[15..18] cache strides, n[19] placement dtype,
 // n[20] w dtype.
+// Fused forms (a verification block's K and V placement of one layer, one
+// launch instead of three): n[21] = 1 places a second cache of the same
+// geometry with the same placement and w -- p[5] cache, p[6] x, p[7] out,
+// n[22..25] that x's strides; n[26] = 1 rotates the first x on load (the
+// RoPE of the keys, k_rope's arithmetic: x1 c - x2 s and x1 s + x2 c in
+// float32, rounded once to the dtype, the value the separate rope step would
+// store), position n[28] + t (+ position[0] from p[9] when n[27] = 1), table
+// p[8] of n[29] rows, a position outside it raising ERR_POSITION and
+// rotating to 0 as k_rope does.
 __global__ void k_kv_place(KArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t KV = a.n[1], C = a.n[2], hd = a.n[3], T = a.n[5];
-  const int64_t row = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= a.n[0] * KV * C) return;
+  const int64_t rows = a.n[0] * KV * C;
+  int64_t row = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= (a.n[21] ? 2 : 1) * rows) return;
+  const bool second = row >= rows;
+  if (second) row -= rows;
+  const bool rope = !second && a.n[26] != 0;
+  const void* cache = a.p[second ? 5 : 0];
+  const void* x = a.p[second ? 6 : 1];
+  void* dst = a.p[second ? 7 : 4];
+  const int64_t* xs = &a.n[second ? 22 : 6];
   const int64_t r = row % C, g = (row / C) % KV, b = row / (C * KV);
   const int dt = static_cast<int>(a.n[4]);
   const int pdt = static_cast<int>(a.n[19]), wdt = static_cast<int>(a.n[20]);
@@ -388,14 +405,35 @@ __global__ void k_kv_place(KArgs a) {
   const int64_t cb = b * a.n[15] + g * a.n[16] + r * a.n[17];
   const int64_t ob = in_place ? cb : row * hd;
   const int64_t od = in_place ? a.n[18] : 1;
+  const int64_t half = hd / 2;
+  const int64_t pos0 = a.n[28] + (rope && a.n[27] == 1 ? static_cast<const int32_t*>(a.p[9])[0] : 0);
   for (int64_t d = lane; d < hd; d += 64) {
     float placed = 0.f;
-    for (int64_t t = 0; t < T; ++t)
-      placed += load_f(a.p[1], b * a.n[6] + g * a.n[7] + t * a.n[8] + d * a.n[9], dt) *
-                load_f(a.p[2], t * a.n[10] + r * a.n[11], pdt);
-    const float c = load_f(a.p[0], cb + d * a.n[18], dt);
+    for (int64_t t = 0; t < T; ++t) {
+      const int64_t xb = b * xs[0] + g * xs[1] + t * xs[2];
+      float v;
+      if (rope) {
+        const int64_t pos = pos0 + t;
+        const int64_t i = d < half ? d : d - half;
+        if (pos >= 0 && pos < a.n[29]) {
+          const float x1 = load_f(x, xb + i * xs[3], dt);
+          const float x2 = load_f(x, xb + (i + half) * xs[3], dt);
+          const float c = load_f(a.p[8], pos * hd + i, dt);
+          const float sn = load_f(a.p[8], pos * hd + half + i, dt);
+          v = round_to(d < half ? __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x2, -sn))
+                                : __fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, c)), dt);
+        } else {
+          if (lane == 0) raise_error(a, ERR_POSITION);
+          v = 0.f;
+        }
+      } else {
+        v = load_f(x, xb + d * xs[3], dt);
+      }
+      placed += v * load_f(a.p[2], t * a.n[10] + r * a.n[11], pdt);
+    }
+    const float c = load_f(cache, cb + d * a.n[18], dt);
     const float kept = round_to(c * round_to(1.f - w, dt), dt);
-    store_f(a.p[4], ob + d * od, dt, round_to(kept + round_to(placed, dt), dt));
+    store_f(dst, ob + d * od, dt, round_to(kept + round_to(placed, dt), dt));
   }
 }
 
@@ -403,10 +441,12 @@ const char* plan_kv_place(KArgs& a, Launch& l) {
   for (int i = 0; i < 4; ++i)
     if (a.n[i] <= 0) return "kv_place: empty dimension";
   if (a.n[5] <= 0) return "kv_place: empty block";
-  const int64_t rows = a.n[0] * a.n[1] * a.n[2];
+  if (a.n[26] != 0 && (a.n[3] % 2 || a.n[29] <= 0)) return "kv_place: RoPE needs an even head size and a table";
+  const int64_t rows = a.n[0] * a.n[1] * a.n[2] * (a.n[21] ? 2 : 1);
   l.func = reinterpret_cast<const void*>(&k_kv_place);
   l.grid = dim3(static_cast<unsigned>((rows + 3) / 4));
   l.block = dim3(256);
+  a.p[kErrPtr] = device_error_word();
   return nullptr;
 }
 

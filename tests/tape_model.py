@@ -374,26 +374,45 @@ def s_kv_write(mem, p, n, f):
 
 def s_kv_place(mem, p, n, f):
     B, KV, C, hd, dt, T = n[0:6]
-    xs = n[6:10]
     pls = n[10:12]
     wsb, wsr, in_place = n[12:15]
     cs = n[15:19]
     pdt, wdt = n[19:21]
+    pair, rope = n[21] if len(n) > 21 else 0, n[26] if len(n) > 26 else 0
+    assert not pair or (p[5][0] >= 0 and p[6][0] >= 0 and p[7][0] >= 0 and p[8][0] >= 0), "paired kv_place unbound"
     pl = load(mem, p[2], pdt, np.arange(T)[:, None] * pls[0] + np.arange(C)[None, :] * pls[1])
-    for b in range(B):
-        w = load(mem, p[3], wdt, b * wsb + np.arange(C) * wsr)
-        touched = (w != 0) | (pl != 0).any(axis=0)
-        for g in range(KV):
-            x = load(mem, p[1], dt, b * xs[0] + g * xs[1] + np.arange(T)[:, None] * xs[2] + np.arange(hd)[None, :] * xs[3])
-            placed = _round((pl.T.astype(np.float64) @ x).astype(np.float32), dt)
-            cidx = b * cs[0] + g * cs[1] + np.arange(C)[:, None] * cs[2] + np.arange(hd)[None, :] * cs[3]
-            c = load(mem, p[0], dt, cidx)
-            new = _round(_round(c * _round(1 - w[:, None], dt), dt) + placed, dt)
-            if in_place:
-                store(mem, p[4], dt, cidx[touched].reshape(-1), new[touched].reshape(-1))
-            else:
-                store(mem, p[4], dt, ((b * KV + g) * C) * hd + np.arange(C * hd), new.reshape(-1))
-    return 0
+    error = 0
+    members = [(p[0], p[1], p[4], n[6:10], bool(rope))]
+    if pair:
+        members.append((p[5], p[6], p[7], n[22:26], False))
+    for cache_p, x_p, out_p, xs, rotate in members:
+        for b in range(B):
+            w = load(mem, p[3], wdt, b * wsb + np.arange(C) * wsr)
+            touched = (w != 0) | (pl != 0).any(axis=0)
+            for g in range(KV):
+                x = load(mem, x_p, dt, b * xs[0] + g * xs[1] + np.arange(T)[:, None] * xs[2] + np.arange(hd)[None, :] * xs[3])
+                if rotate:
+                    # the keys' RoPE on load (k_rope's arithmetic, rounded once)
+                    half = hd // 2
+                    pos = n[28] + np.arange(T) + (int(mem.view(p[9], 3, 1)[0]) if n[27] == 1 else 0)
+                    ok = (pos >= 0) & (pos < n[29])
+                    if not ok.all():
+                        error |= 2
+                    safe = np.where(ok, pos, 0)
+                    c = load(mem, p[8], dt, safe[:, None] * hd + np.arange(half)[None, :])
+                    s = load(mem, p[8], dt, safe[:, None] * hd + half + np.arange(half)[None, :])
+                    x1, x2 = x[:, :half], x[:, half:]
+                    x = _round(np.concatenate([x1 * c + x2 * -s, x1 * s + x2 * c], axis=1), dt)
+                    x[~ok] = 0
+                placed = _round((pl.T.astype(np.float64) @ x).astype(np.float32), dt)
+                cidx = b * cs[0] + g * cs[1] + np.arange(C)[:, None] * cs[2] + np.arange(hd)[None, :] * cs[3]
+                c = load(mem, cache_p, dt, cidx)
+                new = _round(_round(c * _round(1 - w[:, None], dt), dt) + placed, dt)
+                if in_place:
+                    store(mem, out_p, dt, cidx[touched].reshape(-1), new[touched].reshape(-1))
+                else:
+                    store(mem, out_p, dt, ((b * KV + g) * C) * hd + np.arange(C * hd), new.reshape(-1))
+    return error
 
 
 def s_gemv(mem, p, n, f):

@@ -408,7 +408,7 @@ def test_transposed_causal_mask_is_not_treated_as_causal():
 
 
 @pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
-def test_verify_block_plans_row_exact_kernels(dtype):
+def test_verify_block_plans_row_exact_kernels(dtype, monkeypatch):
     """A verification block (5 positions of one sequence, LlamaDecoderBlock):
     its linears are planned row-exact (the single-token step's arithmetic
     per row, RMSNorm as the prologue) and its attention as the read-only
@@ -434,9 +434,18 @@ def test_verify_block_plans_row_exact_kernels(dtype):
     assert source.count("gemv[rms_norm+row_exact]") == 3  # q/k/v of 2 layers + lm_head
     assert source.count("gemv[rms_norm+silu_mul+row_exact]") == 2
     assert source.count("gemv[residual+row_exact]") == 4
+    # rope(k) and both placements of a layer: one paired kv_place
+    assert source.count("kv_place[rope+pair]") == 2 and " rope(" not in source and " kv_place(" not in source
     np.testing.assert_allclose(as_float(got[0]), as_float(expected[0]), atol=3e-2, rtol=2e-2)
     for value, reference in zip(got[1:], expected[1:]):
         np.testing.assert_allclose(as_float(value), as_float(reference), atol=3e-2, rtol=2e-2)
+    # the fused placement computes what rope + two kv_place steps compute, bit for bit
+    from chomikgrad import _planner
+    monkeypatch.setattr(_planner, "fuse_block_kv_place", lambda steps, outputs: steps)
+    unfused, again = model_run(outputs, leaves + caches, donate=caches)
+    assert " rope(" in unfused.source and "kv_place[rope+pair]" not in unfused.source
+    for value, reference in zip(got, again):
+        assert np.array_equal(np.asarray(value).view(np.uint16), np.asarray(reference).view(np.uint16))
 
 
 def as_dtype_host(values, dtype):

@@ -901,8 +901,9 @@ def _producer(steps: List[Step]) -> Dict[int, Tuple[int, Step]]:
 
 def mfma_gemv(step: Step) -> bool:
     """A GEMV the library runs on MFMA (2..16 rows of a 16-bit type, K a
-    multiple of 32, every segment a whole number of 16-column tiles): it takes
-    no RMSNorm prologue, the norm stays its own step."""
+    multiple of 32, every segment a whole number of 16-column tiles).  With
+    an RMSNorm prologue it keeps the whole K in one block (no split over
+    blocks)."""
     x = step.ins[0]
     return (2 <= step.attrs["rows"] <= 16 and x.itemsize == 2 and step.attrs["K"] % 32 == 0
             and not step.attrs.get("exact")
@@ -977,7 +978,7 @@ def fuse_rmsnorm_prologue(steps: List[Step], outputs: List[PV]) -> List[Step]:
         ok = all(
             u.kind == K_GEMV and u.attrs["prologue"] is None and u.ins[0].same_data(normed)
             and u.attrs["rows"] * u.attrs["K"] * normed.itemsize <= GEMV_STAGE_BYTES
-            and not mfma_gemv(u)
+            and (not mfma_gemv(u) or w.dtype == x.dtype)
             and x.row_stride() is not None
             for u in users
         )

@@ -944,8 +944,7 @@ const void* pick_rows(int64_t m, int64_t kv, bool pro, bool silu, bool stage) {
   return pick<T, kMaxRows, 2, 8, 1>(pro, silu, stage);
 }
 
-// Few-row GEMV on MFMA (2 <= M <= 16 input rows, 16-bit types, no RMSNorm
-// prologue: the planner leaves that to k_rmsnorm for these shapes).  With M
+// Few-row GEMV on MFMA (2 <= M <= 16 input rows, 16-bit types).  With M
 // rows every weight element feeds M products, which a VALU kernel cannot
 // keep up with at HBM speed; here each wave computes a 16-column output tile
 // for all rows with v_mfma_f32_16x16x32 (x rows padded to 16 as the A
@@ -954,7 +953,8 @@ const void* pick_rows(int64_t m, int64_t kv, bool pro, bool silu, bool stage) {
 // registers with unconditional (clamped) loads so the waits stay exact.  KS
 // waves of a block split K for one tile and add their partial tiles through
 // LDS.  Epilogues as k_gemv: residual, or the SiLU pair (the gate and up
-// rows of the same columns are two B operands).  Same KArgs layout as k_gemv.
+// rows of the same columns are two B operands); the RMSNorm prologue as
+// described at the kernel.  Same KArgs layout as k_gemv.
 typedef _Float16 mh8v __attribute__((ext_vector_type(8)));
 typedef __bf16 mb8v __attribute__((ext_vector_type(8)));
 typedef float mf4v __attribute__((ext_vector_type(4)));
@@ -972,13 +972,24 @@ template <> struct SkinnyMfma<bf16_t> {
 
 constexpr int kChunk = 4;  // k-steps of 32 per register buffer
 
-template <typename T, int KS, bool SILU>
+// PRO: the RMSNorm prologue (p[1] weight, f[0] eps; only with the whole K in
+// one block).  Before the main loop each wave normalises whole input rows
+// (rows w and w + waves, in one pass) into dynamic LDS, (K / 8 + 1) 16-byte
+// vectors apart
+// so the A-fragment reads of 16 rows hit distinct banks: the rounded squares
+// summed per lane and over the wave, then round(round(x / r) * w) per element
+// with the quotient of k_gemv_row -- the portable graph's rounding points.
+// The A fragments are then read from LDS; the weight stream's first two
+// chunks are issued before the prologue's arithmetic.
+template <typename T, int KS, bool SILU, bool PRO>
 __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) {
   using E = Elem<T>;
   using F = SkinnyMfma<T>;
+  using W = Word<T>;
   constexpr int TPB = KS >= 4 ? 1 : 4 / KS;  // column tiles per block
   constexpr int NB = SILU ? 2 : 1;           // B operands (gate, up)
   __shared__ mf4v red[SILU ? 2 : 1][KS * TPB][64];
+  extern __shared__ uint4 xs[];              // PRO: the normalised input rows
 
   const int M = static_cast<int>(a.n[0]);
   const int64_t K = a.n[1], ldx = a.n[2];
@@ -1015,16 +1026,31 @@ __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) 
   const int64_t steps = K / 32 / KB / KS;   // k-steps of this wave
   const int64_t v0 = (kb * KS + kp) * steps * 4;  // first vector of this wave's k range
   const int64_t vend = v0 + steps * 4;
+  const int64_t xstride = kv + 1;           // PRO: LDS row pitch in vectors
   uint4 xa[2][kChunk], wb[2][NB][kChunk];
-  auto issue = [&](int buf, int64_t c) {
+  // global loads of a chunk (x and weights; the weights only with PRO)
+  auto issue_w = [&](int buf, int64_t c) {
 #pragma unroll
     for (int s = 0; s < kChunk; ++s) {
       const int64_t v = v0 + (c + s) * 4 + fg;  // vector index: 32 columns per step, 8 per lane group
       const int64_t vc = v < vend ? v : vend - 4 + fg;
-      xa[buf][s] = xrow[vc];
+      if (!PRO) xa[buf][s] = xrow[vc];
 #pragma unroll
       for (int b = 0; b < NB; ++b) wb[buf][b][s] = load_w<true>(wrow[b] + vc);
     }
+  };
+  // PRO: the chunk's A fragments from the normalised rows in LDS
+  auto issue_x = [&](int buf, int64_t c) {
+#pragma unroll
+    for (int s = 0; s < kChunk; ++s) {
+      const int64_t v = v0 + (c + s) * 4 + fg;
+      const int64_t vc = v < vend ? v : vend - 4 + fg;
+      xa[buf][s] = xs[xr * xstride + vc];
+    }
+  };
+  auto issue = [&](int buf, int64_t c) {
+    issue_w(buf, c);
+    if (PRO) issue_x(buf, c);
   };
   mf4v acc[NB];
 #pragma unroll
@@ -1038,10 +1064,117 @@ __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) 
       for (int b = 0; b < NB; ++b) acc[b] = F::step(xv, live ? wb[buf][b][s] : zero, acc[b]);
     }
   };
-  (void)kv;
-  issue(0, 0);
+  if constexpr (PRO) {
+    // NW >= 4 waves and M <= 8 rows (checked when planned): rows w and
+    // w + NW of each wave, both in one pass
+    constexpr int NW = KS * TPB;
+    constexpr bool kTwoRows = NW < kMaxRows;
+    constexpr int PV = 4;  // vectors per lane kept in registers: K <= 2048
+    const int r0 = w, r1 = w + NW;
+    const bool has0 = r0 < M, two = kTwoRows && r1 < M;  // wave-uniform
+    const T* x0 = static_cast<const T*>(a.p[0]);
+    const uint4* s0 = reinterpret_cast<const uint4*>(x0 + (has0 ? r0 : 0) * ldx);
+    const uint4* s1 = reinterpret_cast<const uint4*>(x0 + (two ? r1 : has0 ? r0 : 0) * ldx);
+    uint4* d0 = xs + (has0 ? r0 : 0) * xstride;
+    uint4* d1 = xs + (two ? r1 : has0 ? r0 : 0) * xstride;
+    const uint4* nrow = static_cast<const uint4*>(a.p[1]);
+    const int nv = static_cast<int>(kv);
+    const bool in_regs = nv <= 64 * PV;
+    // x and the norm weight first, so their waits do not include the
+    // weight chunks issued after them (loads complete in order)
+    uint4 p0[PV], p1[PV], pg[PV];
+    if (has0 && in_regs) {
+#pragma unroll
+      for (int u = 0; u < PV; ++u) {
+        const int v = lane + 64 * u;
+        const int vc = v < nv ? v : nv - 1;
+        p0[u] = load_x(s0 + vc);
+        if (kTwoRows) p1[u] = load_x(s1 + vc);
+        pg[u] = load_x(nrow + vc);
+      }
+    }
+    issue_w(0, 0);
+    issue_w(1, kChunk);
+    auto divisor = [&](float ss) {
+      const float total = E::round(wave_sum(ss));
+      const float mean = E::round(total / E::round(static_cast<float>(K)));
+      return E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
+    };
+    // round(round(x / r) * g) of one 16-byte vector
+    auto normalise = [&](const uint4& xv, const uint4& gv, float rn, float inv) {
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+      bool fast = W::fast_divisor(rn);
+      if constexpr (!W::kNoBranch) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fast = fast && W::fast_numerator(W::lo(xw[i])) && W::fast_numerator(W::hi(xw[i]));
+      }
+      uint32_t o[4];
+      if (fast) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = W::mul(W::pack(quotient(W::lo(xw[i]), rn, inv), quotient(W::hi(xw[i]), rn, inv)), gw[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = W::lo(xw[i]), hi = W::hi(xw[i]);
+          o[i] = W::kNoBranch ? W::mul(W::pack(lo * inv, hi * inv), gw[i]) : W::mul(W::pack(lo / rn, hi / rn), gw[i]);
+        }
+      }
+      return make_uint4(o[0], o[1], o[2], o[3]);
+    };
+    auto squares = [&](const uint4& xv, float ss) {
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[i], xw[i]), W::kOnes, ss);
+      return ss;
+    };
+    if (has0 && in_regs) {
+      float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+      for (int u = 0; u < PV; ++u) {
+        if (lane + 64 * u < nv) {
+          ss0 = squares(p0[u], ss0);
+          if (kTwoRows) ss1 = squares(p1[u], ss1);
+        }
+      }
+      const float rn0 = divisor(ss0), rn1 = kTwoRows ? divisor(ss1) : 1.f;
+      const float inv0 = 1.0f / rn0, inv1 = 1.0f / rn1;
+#pragma unroll
+      for (int u = 0; u < PV; ++u) {
+        const int v = lane + 64 * u;
+        if (v < nv) {
+          d0[v] = normalise(p0[u], pg[u], rn0, inv0);
+          if (two) d1[v] = normalise(p1[u], pg[u], rn1, inv1);
+        }
+      }
+    } else if (has0) {  // longer rows: raw rows through LDS, then in place
+      float ss0 = 0.f, ss1 = 0.f;
+      for (int v = lane; v < nv; v += 64) {
+        const uint4 a0 = load_x(s0 + v), a1 = load_x(s1 + v);
+        d0[v] = a0;
+        if (two) d1[v] = a1;
+        ss0 = squares(a0, ss0);
+        ss1 = squares(a1, ss1);
+      }
+      const float rn0 = divisor(ss0), rn1 = divisor(ss1);
+      const float inv0 = 1.0f / rn0, inv1 = 1.0f / rn1;
+      for (int v = lane; v < nv; v += 64) {
+        const uint4 gv = load_x(nrow + v);
+        d0[v] = normalise(d0[v], gv, rn0, inv0);
+        if (two) d1[v] = normalise(d1[v], gv, rn1, inv1);
+      }
+    }
+    // every wave's rows are in LDS; the wait covers LDS only (a fence would
+    // drain the weight loads in flight as well), and the asm statement is a
+    // compiler memory barrier
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue_x(0, 0);
+  } else {
+    issue(0, 0);
+  }
   for (int64_t c = 0; c < steps; c += 2 * kChunk) {
-    issue(1, c + kChunk);
+    if (!PRO || c > 0) issue_w(1, c + kChunk);  // PRO: chunk 1's weights went out before the prologue
+    if (PRO) issue_x(1, c + kChunk);
     compute(0, c);
     if (c + kChunk >= steps) break;
     issue(0, c + 2 * kChunk);
@@ -1122,19 +1255,24 @@ __global__ __launch_bounds__(KS >= 4 ? 64 * KS : 256) void k_gemv_mfma(KArgs a) 
 }
 
 template <typename T, int KS>
-const void* pick_mfma_ks(bool silu) {
-  return silu ? reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, true>)
-              : reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, false>);
+const void* pick_mfma_ks(bool silu, bool pro) {
+  if (pro && silu) {  // 16 waves of the SiLU pair with the prologue would spill
+    if constexpr (KS < 16) return reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, true, true>);
+    return nullptr;
+  }
+  if (pro) return reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, false, true>);
+  return silu ? reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, true, false>)
+              : reinterpret_cast<const void*>(&k_gemv_mfma<T, KS, false, false>);
 }
 
 template <typename T>
-const void* pick_mfma(int ks, bool silu) {
+const void* pick_mfma(int ks, bool silu, bool pro) {
   switch (ks) {
-    case 1: return pick_mfma_ks<T, 1>(silu);
-    case 2: return pick_mfma_ks<T, 2>(silu);
-    case 4: return pick_mfma_ks<T, 4>(silu);
-    case 8: return pick_mfma_ks<T, 8>(silu);
-    default: return pick_mfma_ks<T, 16>(silu);
+    case 1: return pick_mfma_ks<T, 1>(silu, pro);
+    case 2: return pick_mfma_ks<T, 2>(silu, pro);
+    case 4: return pick_mfma_ks<T, 4>(silu, pro);
+    case 8: return pick_mfma_ks<T, 8>(silu, pro);
+    default: return pick_mfma_ks<T, 16>(silu, pro);
   }
 }
 
@@ -1869,35 +2007,45 @@ const char* plan_gemv(KArgs& a, Launch& l) {
     l.shmem = 0;
     return nullptr;
   }
-  // 2..16 rows of a 16-bit type without the prologue: the MFMA kernel.
-  // Every segment must be a whole number of 16-column tiles.
+  // 2..16 rows of a 16-bit type: the MFMA kernel.  Every segment must be a
+  // whole number of 16-column tiles; a prologue needs the whole K in one
+  // block and a norm weight of the input's type.
   static const int mfma_knob = env_int("CHOMIK_HIP_GEMV_MFMA", 1);
   bool tiles16 = true;
   for (int s = 0; s < segs; ++s) tiles16 = tiles16 && a.n[7 + s] % 16 == 0;
-  if (mfma_knob && M >= 2 && M <= 16 && !pro && (dt == F16 || dt == BF16) && K % 32 == 0 && tiles16 &&
+  const bool mfma_pro_ok = !pro || (a.n[19] == dt && a.n[24] <= 1);
+  if (mfma_knob && M >= 2 && M <= 16 && mfma_pro_ok && (dt == F16 || dt == BF16) && K % 32 == 0 && tiles16 &&
       a.n[2] % 8 == 0 && aligned) {
     const int64_t cols = silu ? a.n[7] : rows;
     const int64_t tiles = cols / 16;
     // n[24]: blocks sharing a column tile over K (chosen with the workspace
-    // in p[14]); then split each block's K over up to 16 waves while the
-    // launch has fewer than 2048 waves and each wave keeps at least one
-    // register chunk.
+    // in p[14]); then split each block's K over up to 16 waves (8 for the
+    // SiLU pair with the prologue, which would spill at 16) while the launch
+    // has fewer than 2048 waves and each wave keeps at least one register
+    // chunk.
     const int64_t kbs = a.n[24] > 1 ? a.n[24] : 1;
     if ((K / 32) % kbs) return "gemv: K must split evenly over the blocks of a tile";
     if (kbs > 1 && (a.n[25] < tiles * 4 || a.n[25] % 256)) return "gemv: the ticket region must hold one ticket per tile";
     static const int max_ks = env_int("CHOMIK_HIP_GEMV_MFMA_SPLIT", 16);
     const int64_t ksteps = K / 32 / kbs;
     int ks = 1;
-    while (ks < max_ks && ks < 16 && tiles * kbs * ks < 2048 && ksteps % (ks * 2) == 0 && ksteps / (ks * 2) >= kChunk)
+    while (ks < max_ks && ks < (pro && silu ? 8 : 16) && tiles * kbs * ks < 2048 && ksteps % (ks * 2) == 0 && ksteps / (ks * 2) >= kChunk)
       ks *= 2;
+    // the prologue's normalised rows (dynamic) and the partial tiles of the
+    // K split (static) share the block's LDS: at most 64 KiB
+    const size_t pro_lds = pro ? static_cast<size_t>(M) * static_cast<size_t>(K / 8 + 1) * 16 : 0;
+    while (pro && ks > 1 && pro_lds + static_cast<size_t>(silu ? 2 : 1) * (ks >= 4 ? ks : 4) * 1024 > 64 * 1024)
+      ks /= 2;
     const int64_t tpb = ks >= 4 ? 1 : 4 / ks;
+    if (pro && M > 2 * ks * tpb) return "gemv: the prologue normalises at most two rows per wave";
     const int64_t blocks = (tiles + tpb - 1) / tpb * kbs;
     if (blocks > 2147483647) return "gemv: too many rows";
-    l.func = dt == F16 ? pick_mfma<__half>(ks, silu) : pick_mfma<bf16_t>(ks, silu);
+    l.func = dt == F16 ? pick_mfma<__half>(ks, silu, pro) : pick_mfma<bf16_t>(ks, silu, pro);
+    if (!l.func) return "gemv: no MFMA kernel for this split";
     l.grid = dim3(static_cast<unsigned>(blocks));
     l.block = dim3(static_cast<unsigned>(64 * ks * tpb));
     a.p[kErrPtr] = device_error_word();
-    l.shmem = 0;
+    l.shmem = pro_lds;
     return nullptr;
   }
   const int nr = M == 1 ? 1 : 2;

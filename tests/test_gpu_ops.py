@@ -196,6 +196,46 @@ def test_gemv_split_over_blocks(hip, dtype, rows, K, N):
 
 
 @pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("rows,K", [(2, 96), (3, 128), (5, 256), (8, 512), (8, 1024)])
+def test_mfma_gemv_rmsnorm_prologue_equals_separate_norm(hip, dtype, rows, K, monkeypatch):
+    """A batch's RMSNorm folded into the MFMA GEMV as its prologue gives the
+    bits of the separate rms_norm step followed by the same GEMV.  The inputs
+    are multiples of 1/8 in [-2, 2], so every square and every float32 sum
+    of squares is exact in any order and both paths round the same total;
+    the norm weight is not constant, so a misplaced weight or row shows.
+    K = 96 ends inside a register chunk; K = 128 and 256 put two and four
+    column tiles in a block; K = 1024 splits K over eight waves (both paths
+    split K alike at these sizes, so the sums are added in the same order)."""
+    from chomikgrad import _planner
+
+    announce(f"gemv mfma prologue {np.dtype(dtype)} rows={rows} K={K}")
+    rng = np.random.default_rng(K + rows)
+    N = 208  # 13 column tiles: a partial block of tiles where several share a block
+    x = Tensor((rng.integers(-16, 17, size=(rows, 1, K)) / 8).astype(np.float32), dtype=dtype)
+    h = Tensor(rng.normal(size=(rows, 1, N)).astype(np.float32), dtype=dtype)
+    norm = Tensor(rng.normal(1.0, 0.3, size=K).astype(np.float32), dtype=dtype)
+    w1, w2, w3 = (Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype) for _ in range(3))
+    variance = (x * x).mean(axis=-1, keepdims=True)
+    normed = x / (variance + 1e-5).sqrt() * norm
+    normed._node.lowering = ("rms_norm", (x._node, norm._node), 1e-5)
+    gate = normed @ w1.T
+    outputs = [h + normed @ w3.T, gate / (1 + (-gate).exp()) * (normed @ w2.T)]
+    fused = compile_graph(*outputs, compiler="hip")
+    assert " rms_norm(" not in fused.source and fused.source.count("gemv[rms_norm") == 2
+    got = fused()
+    monkeypatch.setattr(_planner, "fuse_rmsnorm_prologue", lambda steps, outputs: steps)
+    monkeypatch.setattr(hip, "_program_cache", {})  # plan again rather than reuse the fused program
+    separate = compile_graph(*outputs, compiler="hip")
+    assert " rms_norm(" in separate.source
+    want = separate()
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(np.asarray(g).view(np.uint16), np.asarray(w).view(np.uint16))
+    expected = realize(*outputs, compiler="cpu")
+    for g, e in zip(got, expected):
+        np.testing.assert_allclose(as_float(g), as_float(e), rtol=3e-2, atol=3e-2)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("shape", [(37, 200, 72), (130, 96, 512), (9, 4100, 264), (2048, 4096, 256)],
                          ids=["ragged", "tall", "wide", "large-tiles"])
 def test_gemm_linear_matches_fp32_reference(hip, dtype, shape):

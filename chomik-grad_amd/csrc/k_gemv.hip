@@ -1636,7 +1636,6 @@ template <typename T, int VPL, bool SILU>
 __global__ __launch_bounds__(256) void k_gemv_exact_run(KArgs a) {
   using E = Elem<T>;
   using W = Word<T>;
-  constexpr int V = 16 / sizeof(T);
   constexpr int KV = 64 * VPL;      // 16-byte vectors per row
   constexpr int RG = SILU ? 2 : 1;  // weight rows per group
   constexpr int WAVES = 4;

@@ -437,13 +437,98 @@ __global__ void k_kv_place(KArgs a) {
   }
 }
 
+// The same placement with the cache, x, placement, w and RoPE table all of
+// one type T: the loads carry no dtype switch, so a row's w and its
+// placement column (kGroup rows at a time) are independent loads in flight
+// together, as are a lane's x (and table) values, instead of one round trip
+// per value.  Same arithmetic, same order: bit-identical to k_kv_place.
+template <typename T>
+__global__ void k_kv_place_t(KArgs a) {
+  using E = Elem<T>;
+  constexpr int kGroup = 8;
+  const int lane = threadIdx.x & 63;
+  const int64_t KV = a.n[1], C = a.n[2], hd = a.n[3], T_ = a.n[5];
+  const int64_t rows = a.n[0] * KV * C;
+  int64_t row = blockIdx.x * int64_t(blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= (a.n[21] ? 2 : 1) * rows) return;
+  const bool second = row >= rows;
+  if (second) row -= rows;
+  const bool rope = !second && a.n[26] != 0;
+  const T* cache = static_cast<const T*>(a.p[second ? 5 : 0]);
+  const T* x = static_cast<const T*>(a.p[second ? 6 : 1]);
+  T* dst = static_cast<T*>(a.p[second ? 7 : 4]);
+  const T* place = static_cast<const T*>(a.p[2]);
+  const T* table = static_cast<const T*>(a.p[8]);
+  const int64_t* xs = &a.n[second ? 22 : 6];
+  const int64_t r = row % C, g = (row / C) % KV, b = row / (C * KV);
+  // the block's first position (RoPE table rows) with the row's w and
+  // placement column: one round trip for all three
+  const int64_t pos0 = a.n[28] + (rope && a.n[27] == 1 ? static_cast<const int32_t*>(a.p[9])[0] : 0);
+  const float w = E::to_f(static_cast<const T*>(a.p[3])[b * a.n[12] + r * a.n[13]]);
+  bool touched = w != 0.f;
+  for (int64_t t0 = 0; t0 < T_; t0 += kGroup) {
+    float pc[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) pc[u] = t0 + u < T_ ? E::to_f(place[(t0 + u) * a.n[10] + r * a.n[11]]) : 0.f;
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) touched |= pc[u] != 0.f;
+  }
+  const bool in_place = a.n[14] != 0;
+  if (in_place && !touched) return;
+  const int64_t cb = b * a.n[15] + g * a.n[16] + r * a.n[17];
+  const int64_t ob = in_place ? cb : row * hd;
+  const int64_t od = in_place ? a.n[18] : 1;
+  const int64_t half = hd / 2;
+  for (int64_t d = lane; d < hd; d += 64) {
+    const float c = E::to_f(cache[cb + d * a.n[18]]);
+    const int64_t i = d < half ? d : d - half;
+    float placed = 0.f;
+    for (int64_t t0 = 0; t0 < T_; t0 += kGroup) {
+      float v[kGroup], pc[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        const int64_t t = t0 + u;
+        const bool valid = t < T_;
+        pc[u] = valid ? E::to_f(place[t * a.n[10] + r * a.n[11]]) : 0.f;
+        const int64_t xb = b * xs[0] + g * xs[1] + (valid ? t : 0) * xs[2];
+        if (rope) {
+          const int64_t pos = pos0 + t;
+          const bool ok = pos >= 0 && pos < a.n[29];
+          const int64_t pc_ = ok ? pos : 0;
+          const float x1 = E::to_f(x[xb + i * xs[3]]);
+          const float x2 = E::to_f(x[xb + (i + half) * xs[3]]);
+          const float cs = E::to_f(table[pc_ * hd + i]);
+          const float sn = E::to_f(table[pc_ * hd + half + i]);
+          v[u] = ok ? E::round(d < half ? __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(x2, -sn))
+                                        : __fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, cs)))
+                    : 0.f;
+          if (valid && !ok && lane == 0) raise_error(a, ERR_POSITION);
+        } else {
+          v[u] = E::to_f(x[xb + d * xs[3]]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u)
+        if (t0 + u < T_) placed += v[u] * pc[u];
+    }
+    const float kept = E::round(c * E::round(1.f - w));
+    dst[ob + d * od] = E::from_f(E::round(kept + E::round(placed)));
+  }
+}
+
 const char* plan_kv_place(KArgs& a, Launch& l) {
   for (int i = 0; i < 4; ++i)
     if (a.n[i] <= 0) return "kv_place: empty dimension";
   if (a.n[5] <= 0) return "kv_place: empty block";
   if (a.n[26] != 0 && (a.n[3] % 2 || a.n[29] <= 0)) return "kv_place: RoPE needs an even head size and a table";
   const int64_t rows = a.n[0] * a.n[1] * a.n[2] * (a.n[21] ? 2 : 1);
-  l.func = reinterpret_cast<const void*>(&k_kv_place);
+  const int dt = static_cast<int>(a.n[4]);
+  const bool one_type = a.n[19] == dt && a.n[20] == dt;
+  l.func = !one_type        ? reinterpret_cast<const void*>(&k_kv_place)
+           : dt == F16      ? reinterpret_cast<const void*>(&k_kv_place_t<__half>)
+           : dt == BF16     ? reinterpret_cast<const void*>(&k_kv_place_t<bf16_t>)
+           : dt == F32      ? reinterpret_cast<const void*>(&k_kv_place_t<float>)
+                            : reinterpret_cast<const void*>(&k_kv_place);
   l.grid = dim3(static_cast<unsigned>((rows + 3) / 4));
   l.block = dim3(256);
   a.p[kErrPtr] = device_error_word();

@@ -1413,6 +1413,31 @@ const char* plan_attn_proj(KArgs& a, Launch& l) {
   return nullptr;
 }
 
+// The wave sums of kMaxRows (8) row slots, RG values each, as one
+// reduce-scatter: offsets 32, 16 and 8 spread the slots over lane bits 5..3
+// (at each step a lane keeps the half its bit selects), then 4, 2 and 1
+// reduce within the slot.  Every slot's sum is wave_sum's butterfly (the same
+// offsets in the same order, each step an IEEE addition of the same two
+// operands), so it is bit-identical to wave_sum of that slot; lane l ends
+// with slot (l >> 3) & 7, in six steps instead of six per slot.
+static_assert(kMaxRows == 8, "the reduce-scatter spreads eight row slots over lane bits 5..3");
+template <int RG>
+__device__ __forceinline__ void scatter_rows(const float (&y)[kMaxRows][2], float (&out)[2]) {
+  const int lane = threadIdx.x & 63;
+  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+  float h[4][RG], q[2][RG];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < RG; ++r) h[i][r] = add_xor_halves<32>(y[i][r], y[i + 4][r], b5);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < RG; ++r) q[i][r] = add_xor_halves<16>(h[i][r], h[i + 2][r], b4);
+#pragma unroll
+  for (int r = 0; r < RG; ++r) out[r] = add_xor<1>(add_xor<2>(add_xor<4>(add_xor_halves<8>(q[0][r], q[1][r], b3))));
+}
+
 // Row-exact few-row GEMV (2..8 rows of a 16-bit type, the positions of one
 // sequence: a speculative verification block).  Every output row is computed
 // with exactly the arithmetic of the single-row decode kernel the same
@@ -1601,24 +1626,28 @@ __global__ __launch_bounds__(exact_threads(VPL)) void k_gemv_exact(KArgs a) {
     }
   }
 
+  // the wave sums of every row at once; lane l finishes row (l >> 3) & 7
+  float y[kMaxRows][2];
 #pragma unroll
-  for (int m = 0; m < kMaxRows; ++m) {
-    if (m >= M) break;
-    float y[2];
+  for (int m = 0; m < kMaxRows; ++m)
 #pragma unroll
-    for (int r = 0; r < 2; ++r) y[r] = r < RG ? wave_sum(two ? acc[m][r] + acc2[m][r] : acc[m][r]) : 0.f;
-    if (silu) {
-      const float g = E::round(y[0]);
-      const float u = E::round(y[1]);
-      const float denom = E::round(E::round(expf(-g)) + 1.f);
-      const T out = E::from_f(E::round(E::round(g / denom) * u));
-      if (lane == 0) static_cast<T*>(a.p[6])[m * a.n[11] + idx[0]] = out;
-    } else {
-      float v = E::round(y[0]);
-      const T* res = st.residual(seg[0]);
-      if (res) v = E::round(E::to_f(res[m * st.res_stride(seg[0]) + idx[0]]) + v);
-      if (lane == 0) st.output(seg[0])[m * st.out_stride(seg[0]) + idx[0]] = E::from_f(v);
-    }
+    for (int r = 0; r < 2; ++r) y[m][r] = (m < M && r < RG) ? (two ? acc[m][r] + acc2[m][r] : acc[m][r]) : 0.f;
+  float z[2];
+  const int mr = (lane >> 3) & 7;
+  const bool store = (lane & 7) == 0 && mr < M;
+  if (silu) {
+    scatter_rows<2>(y, z);
+    const float g = E::round(z[0]);
+    const float u = E::round(z[1]);
+    const float denom = E::round(E::round(expf(-g)) + 1.f);
+    const T out = E::from_f(E::round(E::round(g / denom) * u));
+    if (store) static_cast<T*>(a.p[6])[mr * a.n[11] + idx[0]] = out;
+  } else {
+    scatter_rows<1>(y, z);
+    float v = E::round(z[0]);
+    const T* res = st.residual(seg[0]);
+    if (res) v = E::round(E::to_f(res[(mr < M ? mr : 0) * st.res_stride(seg[0]) + idx[0]]) + v);
+    if (store) st.output(seg[0])[mr * st.out_stride(seg[0]) + idx[0]] = E::from_f(v);
   }
 }
 
@@ -1681,8 +1710,9 @@ __global__ __launch_bounds__(256) void k_gemv_exact_run(KArgs a) {
     uint4 w[RG][VPL];
     int seg;
     int64_t idx;
-    float res[kMaxRows];
+    float res;  // the residual of row (lane >> 3) & 7, which this lane finishes
   };
+  const int mr = (lane >> 3) & 7;
   // Every load is unconditional (a row past M, or a segment without a
   // residual, reads x[0] and discards it) so the wait counts stay exact.
   auto issue = [&](Group& b, int g) {
@@ -1698,11 +1728,8 @@ __global__ __launch_bounds__(256) void k_gemv_exact_run(KArgs a) {
       wp[0] = reinterpret_cast<const uint4*>(st.weight(b.seg) + b.idx * K);
       const T* r = st.residual(b.seg);
       const int64_t rs = st.res_stride(b.seg);
-#pragma unroll
-      for (int m = 0; m < kMaxRows; ++m) {
-        const T* src = (r && m < M) ? r + m * rs + b.idx : static_cast<const T*>(a.p[0]);
-        b.res[m] = E::to_f(*src);
-      }
+      const T* src = (r && mr < M) ? r + mr * rs + b.idx : static_cast<const T*>(a.p[0]);
+      b.res = E::to_f(*src);
     }
 #pragma unroll
     for (int r = 0; r < RG; ++r)
@@ -1783,7 +1810,11 @@ __global__ __launch_bounds__(256) void k_gemv_exact_run(KArgs a) {
   // rows' chains interleave measured slower: the kernel is bound by its
   // VALU work, which that adds to.)
   auto finish = [&](const Group& b) {
-    float y[kMaxRows][RG];
+    float y[kMaxRows][2];
+#pragma unroll
+    for (int m = 0; m < kMaxRows; ++m)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) y[m][r] = 0.f;
 #pragma unroll
     for (int m = 0; m < kMaxRows; ++m) {
       if (m >= M) break;
@@ -1808,7 +1839,7 @@ __global__ __launch_bounds__(256) void k_gemv_exact_run(KArgs a) {
             s0 = W::dot(xw[u][2], ww[2], s0);
             s1 = W::dot(xw[u][3], ww[3], s1);
           }
-          y[m][r] = wave_sum(s0 + s1);
+          y[m][r] = s0 + s1;
         } else {
 #pragma unroll
           for (int u = 0; u < VPL; ++u) {
@@ -1816,24 +1847,24 @@ __global__ __launch_bounds__(256) void k_gemv_exact_run(KArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) s0 = W::dot(xw[u][i], ww[i], s0);
           }
-          y[m][r] = wave_sum(s0);
+          y[m][r] = s0;
         }
       }
     }
-#pragma unroll
-    for (int m = 0; m < kMaxRows; ++m) {
-      if (m >= M) break;
-      if (SILU) {
-        const float g = E::round(y[m][0]);
-        const float u = E::round(y[m][RG - 1]);
-        const float denom = E::round(E::round(expf(-g)) + 1.f);
-        const T out = E::from_f(E::round(E::round(g / denom) * u));
-        if (lane == 0) static_cast<T*>(a.p[6])[m * a.n[11] + b.idx] = out;
-      } else {
-        float v = E::round(y[m][0]);
-        if (st.residual(b.seg)) v = E::round(b.res[m] + v);
-        if (lane == 0) st.output(b.seg)[m * st.out_stride(b.seg) + b.idx] = E::from_f(v);
-      }
+    // the wave sums of every row at once; this lane finishes row mr
+    float z[2];
+    scatter_rows<RG>(y, z);
+    const bool store = (lane & 7) == 0 && mr < M;
+    if (SILU) {
+      const float g = E::round(z[0]);
+      const float u = E::round(z[RG - 1]);
+      const float denom = E::round(E::round(expf(-g)) + 1.f);
+      const T out = E::from_f(E::round(E::round(g / denom) * u));
+      if (store) static_cast<T*>(a.p[6])[mr * a.n[11] + b.idx] = out;
+    } else {
+      float v = E::round(z[0]);
+      if (st.residual(b.seg)) v = E::round(b.res + v);
+      if (store) st.output(b.seg)[mr * st.out_stride(b.seg) + b.idx] = E::from_f(v);
     }
   };
   // 32-bit group indices (row counts stay far below 2^31): scalar compares;

@@ -226,7 +226,26 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
 // two blocks per CU, which measured faster than four stages at one block.  Out-of-range rows read a
 // clamped row (their results are not stored); K must be a multiple of the
 // 64-column stage.  Same arguments, epilogues and tile order as k_gemm_nt.
-template <typename T, int BM, int BN, bool SILU, bool RES>
+// lds_load16 issued as inline assembly (M0 set by the compiler through the
+// operand constraint; the s_nop covers the M0-write hazard).  The compiler
+// does not track these transfers, so it adds no wait for them before LDS
+// reads: with the builtin it drained the next stage's loads (vmcnt(0))
+// before the first fragment read of the current stage, because it cannot
+// tell the two stage buffers apart, and no prefetch overlapped any MFMA.
+// The kernel's own s_waitcnt at the top of each stage orders them; every
+// other global load of the kernel comes after the last of them is waited for.
+__device__ __forceinline__ void lds_load16_untracked(const void* global, void* lds) {
+  const uint32_t offset = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)(static_cast<char*>(lds))));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(global), "{m0}"(offset) : "memory");
+}
+
+// UT: stage loads through lds_load16_untracked, so the next stage's loads
+// overlap the current stage's MFMAs (C3 q/k/v 42.8 -> 33.5 us, gate/up
+// 139 -> 127 us); without it the builtin's drain stays, which measured
+// faster for 64 x 64 tiles over a long K (down, K = 5632: 82 against
+// 91 us), where L2 -> LDS traffic rather than latency bounds the kernel.
+template <typename T, int BM, int BN, bool SILU, bool RES, bool UT>
 __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
   using E = Elem<T>;
   constexpr int S = kStages;
@@ -296,9 +315,15 @@ __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
   }
   auto load_stage = [&](int64_t k0, int b) {
 #pragma unroll
-    for (int j = 0; j < AI; ++j) lds_load16(asrc[j] + k0, &As[b][(wave * AI + j) * 64]);
+    for (int j = 0; j < AI; ++j) {
+      if constexpr (UT) lds_load16_untracked(asrc[j] + k0, &As[b][(wave * AI + j) * 64]);
+      else lds_load16(asrc[j] + k0, &As[b][(wave * AI + j) * 64]);
+    }
 #pragma unroll
-    for (int j = 0; j < WI; ++j) lds_load16(wsrc[j] + k0, &Ws[b][(wave * WI + j) * 64]);
+    for (int j = 0; j < WI; ++j) {
+      if constexpr (UT) lds_load16_untracked(wsrc[j] + k0, &Ws[b][(wave * WI + j) * 64]);
+      else lds_load16(wsrc[j] + k0, &Ws[b][(wave * WI + j) * 64]);
+    }
   };
 
   f4v acc[TM][TN];
@@ -380,18 +405,19 @@ __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
 }
 
 template <typename T, bool SILU, bool RES>
-const void* pick_gemm_tile(bool big, bool lds) {
+const void* pick_gemm_tile(bool big, bool lds, bool long_k) {
   if (lds)
-    return big ? reinterpret_cast<const void*>(&k_gemm_lds<T, 128, 128, SILU, RES>)
-               : reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES>);
+    return big       ? reinterpret_cast<const void*>(&k_gemm_lds<T, 128, 128, SILU, RES, true>)
+           : long_k  ? reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES, false>)
+                     : reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES, true>);
   return big ? reinterpret_cast<const void*>(&k_gemm_nt<T, 128, 128, SILU, RES>)
              : reinterpret_cast<const void*>(&k_gemm_nt<T, 64, 64, SILU, RES>);
 }
 
 template <typename T>
-const void* pick_gemm(bool big, bool silu, bool res, bool lds) {
-  if (silu) return pick_gemm_tile<T, true, false>(big, lds);
-  return res ? pick_gemm_tile<T, false, true>(big, lds) : pick_gemm_tile<T, false, false>(big, lds);
+const void* pick_gemm(bool big, bool silu, bool res, bool lds, bool long_k) {
+  if (silu) return pick_gemm_tile<T, true, false>(big, lds, long_k);
+  return res ? pick_gemm_tile<T, false, true>(big, lds, long_k) : pick_gemm_tile<T, false, false>(big, lds, long_k);
 }
 
 const char* plan_gemm(KArgs& a, Launch& l) {
@@ -438,7 +464,8 @@ const char* plan_gemm(KArgs& a, Launch& l) {
     return v && *v ? std::atoi(v) : 1;
   }();
   const bool lds = lds_knob != 0 && K % kBK == 0;
-  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res, lds) : pick_gemm<bf16_t>(big, silu, res, lds);
+  const bool long_k = K >= 4096;
+  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res, lds, long_k) : pick_gemm<bf16_t>(big, silu, res, lds, long_k);
   l.grid = dim3(static_cast<unsigned>(blocks));
   l.block = dim3(256);
   l.shmem = 0;

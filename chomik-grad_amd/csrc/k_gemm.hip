@@ -245,14 +245,22 @@ __device__ __forceinline__ void lds_load16_untracked(const void* global, void* l
 // 139 -> 127 us); without it the builtin's drain stays, which measured
 // faster for 64 x 64 tiles over a long K (down, K = 5632: 82 against
 // 91 us), where L2 -> LDS traffic rather than latency bounds the kernel.
-template <typename T, int BM, int BN, bool SILU, bool RES, bool UT>
-__global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
+//
+// WM x WN waves of BM / WM x BN / WN wave tiles and S stages: 2 x 2 waves
+// and two stages for the 128 x 128 and 64 x 64 tiles (two blocks per CU);
+// 4 x 2 waves and three 48 KiB stages for 256 x 128 (one block per CU, a
+// quarter fewer bytes per flop, two stages in flight): C3 gate/up 125 ->
+// 119 us.  More stages at 128 x 128 (one block per CU) measured slower.
+template <typename T, int BM, int BN, bool SILU, bool RES, bool UT, int WM = 2, int WN = 2, int S = kStages>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(KArgs a) {
   using E = Elem<T>;
-  constexpr int S = kStages;
+  constexpr int NT = 64 * WM * WN;
   constexpr int ON = SILU ? BN / 2 : BN;
-  constexpr int TM = BM / 2 / 16, TN = BN / 2 / 16;
-  constexpr int AI = BM * 8 / 256, WI = BN * 8 / 256;  // 1 KiB instructions per wave per stage
-  static_assert(AI >= 1 && WI >= 1, "tile too small for 256 threads");
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int AI = BM * 8 / NT, WI = BN * 8 / NT;
+  static_assert(AI >= 1 && WI >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0, "tile too small for the block");
+  static_assert(!SILU || TN % 2 == 0, "the SiLU pair needs gate and up fragments in every wave");
+  static_assert(S >= 2 && S <= 4, "the stage waits cover two to four stages");
   __shared__ __attribute__((aligned(1024))) uint4 As[S][BM * 8];
   __shared__ __attribute__((aligned(1024))) uint4 Ws[S][BN * 8];
 
@@ -286,7 +294,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int fi = lane & 15, fg = lane >> 4;
 
   // the source of each lane's vector: instruction j of this wave covers tile
@@ -355,12 +363,12 @@ __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
       const int c = ks * 4 + fg;  // logical chunk of this lane's eight k values
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int r = wm * (BM / 2) + i * 16 + fi;
+        const int r = wm * (BM / WM) + i * 16 + fi;
         fa[i] = As[buf][r * 8 + (c ^ ((r >> 1) & 7))];
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const int r = wn * (BN / 2) + j * 16 + fi;
+        const int r = wn * (BN / WN) + j * 16 + fi;
         fw[j] = Ws[buf][r * 8 + (c ^ ((r >> 1) & 7))];
       }
 #pragma unroll
@@ -378,7 +386,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
         const int64_t n = n0 + 16 * ((wn * TN + j) >> 1) + fi;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int64_t m = m0 + wm * (BM / 2) + i * 16 + fg * 4 + r;
+          const int64_t m = m0 + wm * (BM / WM) + i * 16 + fg * 4 + r;
           const float g = E::round(acc[i][j][r]);
           const float u = E::round(acc[i][j + 1][r]);
           const float denom = E::round(E::round(expf(-g)) + 1.f);
@@ -391,10 +399,10 @@ __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int64_t n = n0 + wn * (BN / 2) + j * 16 + fi;
+      const int64_t n = n0 + wn * (BN / WN) + j * 16 + fi;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + wm * (BM / 2) + i * 16 + fg * 4 + r;
+        const int64_t m = m0 + wm * (BM / WM) + i * 16 + fg * 4 + r;
         if (m < M && n < N) {
           float y = E::round(acc[i][j][r]);
           if (RES) y = E::round(E::to_f(R[m * ldr + n]) + y);
@@ -405,7 +413,8 @@ __global__ __launch_bounds__(256) void k_gemm_lds(KArgs a) {
 }
 
 template <typename T, bool SILU, bool RES>
-const void* pick_gemm_tile(bool big, bool lds, bool long_k) {
+const void* pick_gemm_tile(bool big, bool lds, bool long_k, bool huge) {
+  if (lds && huge) return reinterpret_cast<const void*>(&k_gemm_lds<T, 256, 128, SILU, RES, true, 4, 2, 3>);
   if (lds)
     return big       ? reinterpret_cast<const void*>(&k_gemm_lds<T, 128, 128, SILU, RES, true>)
            : long_k  ? reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES, false>)
@@ -415,9 +424,9 @@ const void* pick_gemm_tile(bool big, bool lds, bool long_k) {
 }
 
 template <typename T>
-const void* pick_gemm(bool big, bool silu, bool res, bool lds, bool long_k) {
-  if (silu) return pick_gemm_tile<T, true, false>(big, lds, long_k);
-  return res ? pick_gemm_tile<T, false, true>(big, lds, long_k) : pick_gemm_tile<T, false, false>(big, lds, long_k);
+const void* pick_gemm(bool big, bool silu, bool res, bool lds, bool long_k, bool huge) {
+  if (silu) return pick_gemm_tile<T, true, false>(big, lds, long_k, huge);
+  return res ? pick_gemm_tile<T, false, true>(big, lds, long_k, huge) : pick_gemm_tile<T, false, false>(big, lds, long_k, huge);
 }
 
 const char* plan_gemm(KArgs& a, Launch& l) {
@@ -465,9 +474,20 @@ const char* plan_gemm(KArgs& a, Launch& l) {
   }();
   const bool lds = lds_knob != 0 && K % kBK == 0;
   const bool long_k = K >= 4096;
-  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res, lds, long_k) : pick_gemm<bf16_t>(big, silu, res, lds, long_k);
-  l.grid = dim3(static_cast<unsigned>(blocks));
-  l.block = dim3(256);
+  // 256 x 128 tiles once there are at least CHOMIK_HIP_GEMM_HUGE_TILES (512)
+  // of them: C3's gate/up (704); 0 never
+  static const int64_t huge_from = [] {
+    const char* v = std::getenv("CHOMIK_HIP_GEMM_HUGE_TILES");
+    return v && *v ? std::atoll(v) : 512;
+  }();
+  const int64_t huge_tiles = ((M + 255) / 256) * ((N * span + 127) / 128);
+  const bool huge = lds && huge_from > 0 && huge_tiles >= huge_from;
+  const int64_t hbm = huge ? 256 : bm, hon = huge ? 128 / span : on;
+  const int64_t launch_tiles = ((M + hbm - 1) / hbm) * ((N + hon - 1) / hon);
+  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res, lds, long_k, huge) : pick_gemm<bf16_t>(big, silu, res, lds, long_k, huge);
+  if (8 * ((launch_tiles + 7) / 8) > 2147483647) return "gemm: too many tiles";
+  l.grid = dim3(static_cast<unsigned>(8 * ((launch_tiles + 7) / 8)));
+  l.block = dim3(huge ? 512 : 256);
   l.shmem = 0;
   return nullptr;
 }

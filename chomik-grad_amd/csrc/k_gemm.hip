@@ -412,21 +412,27 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(KArgs a) {
     }
 }
 
+// Block shapes of the straight-to-LDS kernel (tile, waves, stages).
+enum GemmTile { kTile64, kTile128, kTile128x8, kTile256x8 };
+
 template <typename T, bool SILU, bool RES>
-const void* pick_gemm_tile(bool big, bool lds, bool long_k, bool huge) {
-  if (lds && huge) return reinterpret_cast<const void*>(&k_gemm_lds<T, 256, 128, SILU, RES, true, 4, 2, 3>);
-  if (lds)
-    return big       ? reinterpret_cast<const void*>(&k_gemm_lds<T, 128, 128, SILU, RES, true>)
-           : long_k  ? reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES, false>)
-                     : reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES, true>);
-  return big ? reinterpret_cast<const void*>(&k_gemm_nt<T, 128, 128, SILU, RES>)
-             : reinterpret_cast<const void*>(&k_gemm_nt<T, 64, 64, SILU, RES>);
+const void* pick_gemm_tile(GemmTile tile, bool lds, bool long_k) {
+  if (lds) switch (tile) {
+      case kTile256x8: return reinterpret_cast<const void*>(&k_gemm_lds<T, 256, 128, SILU, RES, true, 4, 2, 3>);
+      case kTile128x8: return reinterpret_cast<const void*>(&k_gemm_lds<T, 128, 128, SILU, RES, true, 4, 2, 3>);
+      case kTile128: return reinterpret_cast<const void*>(&k_gemm_lds<T, 128, 128, SILU, RES, true>);
+      default:
+        return long_k ? reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES, false>)
+                      : reinterpret_cast<const void*>(&k_gemm_lds<T, 64, 64, SILU, RES, true>);
+    }
+  return tile == kTile128 ? reinterpret_cast<const void*>(&k_gemm_nt<T, 128, 128, SILU, RES>)
+                          : reinterpret_cast<const void*>(&k_gemm_nt<T, 64, 64, SILU, RES>);
 }
 
 template <typename T>
-const void* pick_gemm(bool big, bool silu, bool res, bool lds, bool long_k, bool huge) {
-  if (silu) return pick_gemm_tile<T, true, false>(big, lds, long_k, huge);
-  return res ? pick_gemm_tile<T, false, true>(big, lds, long_k, huge) : pick_gemm_tile<T, false, false>(big, lds, long_k, huge);
+const void* pick_gemm(GemmTile tile, bool silu, bool res, bool lds, bool long_k) {
+  if (silu) return pick_gemm_tile<T, true, false>(tile, lds, long_k);
+  return res ? pick_gemm_tile<T, false, true>(tile, lds, long_k) : pick_gemm_tile<T, false, false>(tile, lds, long_k);
 }
 
 const char* plan_gemm(KArgs& a, Launch& l) {
@@ -450,22 +456,23 @@ const char* plan_gemm(KArgs& a, Launch& l) {
     }
     if (total != N) return "gemm: segment widths must add up to N";
   }
-  // 128 x 128 tiles once they outnumber the 256 CUs, else 64 x 64 (output
-  // tiles are half as wide with the SiLU pair).  Measured at C3: the q/k/v
-  // GEMM (320 big tiles) 55 -> 45 us with big tiles, the o and down GEMMs
-  // (exactly 256) 39 -> 46 and 100 -> 108 us, so 256 stay small.
-  // CHOMIK_HIP_GEMM_BIG_TILES moves the threshold.
-  static const int64_t big_from = [] {
-    const char* v = std::getenv("CHOMIK_HIP_GEMM_BIG_TILES");
-    return v && *v ? std::atoll(v) : 257;
-  }();
-  const int64_t span = silu ? 2 : 1;
-  const int64_t big_tiles = ((M + 127) / 128) * ((N * span + 127) / 128);
-  const bool big = big_tiles >= big_from;
-  const int64_t bm = big ? 128 : 64, on = bm / span;
-  const int64_t tiles = ((M + bm - 1) / bm) * ((N + on - 1) / on);
-  const int64_t blocks = 8 * ((tiles + 7) / 8);
-  if (blocks > 2147483647) return "gemm: too many tiles";
+  // Tile choice by the number of tiles (output tiles are half as wide with
+  // the SiLU pair), measured at C3 (2048 tokens):
+  //  * >= 512 tiles of 256 x 128 (CHOMIK_HIP_GEMM_HUGE_TILES; 0 never):
+  //    8 waves, three stages, one block per CU -- gate/up (704) 125 -> 115 us;
+  //  * >= 257 tiles of 128 x 128 (CHOMIK_HIP_GEMM_BIG_TILES): 4 waves, two
+  //    stages, two blocks per CU -- q/k/v (320) 33 us (39 with 8 waves);
+  //  * 224..256 tiles of 128 x 128 (CHOMIK_HIP_GEMM_MID_TILES, the lower
+  //    bound): 8 waves, three stages, one block per CU -- o and down
+  //    (exactly 256) 32.1 -> 26.8 us and 83 -> 63 us against 64 x 64;
+  //  * else 64 x 64 (4 waves, two stages).
+  auto env_tiles = [](const char* name, int64_t fallback) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoll(v) : fallback;
+  };
+  static const int64_t big_from = env_tiles("CHOMIK_HIP_GEMM_BIG_TILES", 257);
+  static const int64_t mid_from = env_tiles("CHOMIK_HIP_GEMM_MID_TILES", 224);
+  static const int64_t huge_from = env_tiles("CHOMIK_HIP_GEMM_HUGE_TILES", 512);
   // straight-to-LDS tiles when K is a whole number of 64-column stages
   // (CHOMIK_HIP_GEMM_LDS=0 keeps the register-staged kernel)
   static const int lds_knob = [] {
@@ -474,20 +481,21 @@ const char* plan_gemm(KArgs& a, Launch& l) {
   }();
   const bool lds = lds_knob != 0 && K % kBK == 0;
   const bool long_k = K >= 4096;
-  // 256 x 128 tiles once there are at least CHOMIK_HIP_GEMM_HUGE_TILES (512)
-  // of them: C3's gate/up (704); 0 never
-  static const int64_t huge_from = [] {
-    const char* v = std::getenv("CHOMIK_HIP_GEMM_HUGE_TILES");
-    return v && *v ? std::atoll(v) : 512;
-  }();
+  const int64_t span = silu ? 2 : 1;
+  const int64_t big_tiles = ((M + 127) / 128) * ((N * span + 127) / 128);
   const int64_t huge_tiles = ((M + 255) / 256) * ((N * span + 127) / 128);
-  const bool huge = lds && huge_from > 0 && huge_tiles >= huge_from;
-  const int64_t hbm = huge ? 256 : bm, hon = huge ? 128 / span : on;
-  const int64_t launch_tiles = ((M + hbm - 1) / hbm) * ((N + hon - 1) / hon);
-  l.func = dt == F16 ? pick_gemm<__half>(big, silu, res, lds, long_k, huge) : pick_gemm<bf16_t>(big, silu, res, lds, long_k, huge);
-  if (8 * ((launch_tiles + 7) / 8) > 2147483647) return "gemm: too many tiles";
-  l.grid = dim3(static_cast<unsigned>(8 * ((launch_tiles + 7) / 8)));
-  l.block = dim3(huge ? 512 : 256);
+  GemmTile tile = kTile64;
+  if (lds && huge_from > 0 && huge_tiles >= huge_from) tile = kTile256x8;
+  else if (big_tiles >= big_from) tile = kTile128;
+  else if (lds && big_tiles >= mid_from) tile = kTile128x8;
+  const int64_t bm = tile == kTile256x8 ? 256 : tile == kTile64 ? 64 : 128;
+  const int64_t on = (tile == kTile64 ? 64 : 128) / span;
+  const int64_t tiles = ((M + bm - 1) / bm) * ((N + on - 1) / on);
+  const int64_t blocks = 8 * ((tiles + 7) / 8);
+  if (blocks > 2147483647) return "gemm: too many tiles";
+  l.func = dt == F16 ? pick_gemm<__half>(tile, silu, res, lds, long_k) : pick_gemm<bf16_t>(tile, silu, res, lds, long_k);
+  l.grid = dim3(static_cast<unsigned>(blocks));
+  l.block = dim3(lds && (tile == kTile256x8 || tile == kTile128x8) ? 512 : 256);
   l.shmem = 0;
   return nullptr;
 }

@@ -237,14 +237,15 @@ def test_mfma_gemv_rmsnorm_prologue_equals_separate_norm(hip, dtype, rows, K, mo
 
 @pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("shape", [(37, 200, 72), (130, 96, 512), (9, 4100, 264), (2048, 4096, 256),
-                                   (1000, 16384, 320)],
-                         ids=["ragged", "tall", "wide", "large-tiles", "8-wave-tiles"])
+                                   (1000, 16384, 320), (2000, 2048, 192)],
+                         ids=["ragged", "tall", "wide", "large-tiles", "8-wave-tiles", "8-wave-128-tiles"])
 def test_gemm_linear_matches_fp32_reference(hip, dtype, shape):
     """Linears with more than 8 rows run the MFMA GEMM (K_GEMM): fp32
     accumulation of the 16-bit operands and one rounding, against a float32
     matmul of the same rounded inputs.  Shapes cover ragged M/N/K edges, the
-    64x64, 128x128 and 8-wave 256x128 tiles (512 of those: 4 x 128, the last
-    row of tiles ragged), and K a multiple of 8 but not of the 64-column
+    64x64 and 128x128 tiles, the 8-wave 256x128 tiles (512 of those: 4 x
+    128, the last row of tiles ragged) and 8-wave 128x128 tiles (256, the
+    last row ragged), and K a multiple of 8 but not of the 64-column
     stage."""
     M, N, K = shape
     announce(f"gemm {dtype_name(dtype)} M={M} N={N} K={K}")

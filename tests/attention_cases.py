@@ -38,6 +38,7 @@ CASES: List[Case] = [
     Case("g1-fractional-per-head-fp16", np.float16, 3, 8, 8, 100, [99, 0, 50], write="fractional", mask="per_head"),
     Case("g4-short-bf16", BFLOAT16, 1, 8, 2, 37, [36]),
     Case("g2-fractional-fp32", np.float32, 2, 4, 2, 70, [3, 69], write="fractional", mask="per_head"),
+    Case("g2-fractional-per-head-bf16", BFLOAT16, 2, 8, 4, 150, [149, 6], write="fractional", mask="per_head"),
 ]
 
 

@@ -24,19 +24,22 @@ def as_float(values):
     return bf16_to_float32(values) if values.dtype == BFLOAT16 else values.astype(np.float32)
 
 
-@pytest.mark.parametrize("passes", [0, 1, 4, -2, "stream8", "stream768"])
+@pytest.mark.parametrize("passes", [0, 1, 4, -2, "stream8", "stream768", "stream8-u4"])
 @pytest.mark.parametrize("case", attention_cases.CASES, ids=lambda c: c.name)
 def test_decode_attention_matches_oracle(hip, case, passes, monkeypatch):
     """passes: the chunk kernel's passes per workgroup (0 = chosen), -2 the
     MFMA kernel where it applies (16-bit caches of at most 768 rows), or the
     streaming kernel aiming at 8 workgroups (one or two ranges per KV head,
-    many tiles) or 768 (many short ranges, combined)."""
+    many tiles) or 768 (many short ranges, combined), with two passes per
+    tile or, for "-u4", four."""
     from chomikgrad import _planner
 
     print(f"[gpu case] decode attention {case.name} passes={passes}", flush=True)
     if isinstance(passes, str):
+        wgs, _, unroll = passes[len("stream"):].partition("-u")
         monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", -1)
-        monkeypatch.setattr(_planner, "DECODE_ATTN_STREAM_WGS", int(passes[len("stream"):]))
+        monkeypatch.setattr(_planner, "DECODE_ATTN_STREAM_WGS", int(wgs))
+        monkeypatch.setattr(_planner, "DECODE_ATTN_STREAM_UNROLL", int(unroll or 2))
     else:
         monkeypatch.setattr(_planner, "DECODE_ATTN_PASSES", passes)
     outputs, dynamic, caches = attention_cases.build(case)

@@ -4,8 +4,9 @@
 // dtype -- the result np.matmul gives for half-precision operands.
 //
 // Both operands are k-contiguous (A row-major with row stride lda, W in its
-// HF (out, in) layout), so every lane loads 16-byte vectors along k.  A block
-// of 256 threads (2 x 2 wavefronts) computes a BM x BN tile with
+// HF (out, in) layout), so every lane loads 16-byte vectors along k.  In the
+// register-staged kernel (k_gemm_nt, used when K is not a whole number of
+// 64-column stages) a block of 256 threads (2 x 2 wavefronts) computes a BM x BN tile with
 // v_mfma_f32_16x16x32 steps; A and W tiles of BK = 64 columns go through a
 // double-buffered LDS stage (rows padded by 16 bytes so the 16 rows a
 // fragment read touches fall in distinct banks), one barrier per stage, the
@@ -36,7 +37,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int kBK = 64;            // k columns per LDS stage
 constexpr int kPad = 8;            // elements of padding per LDS row
 constexpr int kRow = kBK + kPad;   // LDS row length (elements)
-constexpr int kStages = 2;         // LDS stages of the straight-to-LDS kernel (4: one block per CU, slower)
+constexpr int kStages = 2;         // LDS stages of the 4-wave straight-to-LDS tiles
 
 template <typename T> struct Mfma;
 template <> struct Mfma<__half> {
@@ -221,11 +222,11 @@ __global__ __launch_bounds__(256) void k_gemm_nt(KArgs a) {
 // position c ^ ((r >> 1) & 7), so the 16 rows an MFMA fragment read touches
 // at one chunk fall in 16 distinct groups of 4 banks (rows of one parity
 // differ in the swizzle, the two parities in the half of the 128-byte row).
-// kStages stages of LDS keep kStages - 1 stages of loads in flight, one
-// barrier per stage; two stages (64 KiB at 128 x 128 tiles) leave room for
-// two blocks per CU, which measured faster than four stages at one block.  Out-of-range rows read a
-// clamped row (their results are not stored); K must be a multiple of the
-// 64-column stage.  Same arguments, epilogues and tile order as k_gemm_nt.
+// S stages of LDS keep S - 1 stages of loads in flight, one barrier per
+// stage.  Out-of-range rows read a clamped row (their results are not
+// stored); K must be a multiple of the 64-column stage.  Same arguments,
+// epilogues and tile order as k_gemm_nt.
+//
 // lds_load16 issued as inline assembly (M0 set by the compiler through the
 // operand constraint; the s_nop covers the M0-write hazard).  The compiler
 // does not track these transfers, so it adds no wait for them before LDS
@@ -247,10 +248,12 @@ __device__ __forceinline__ void lds_load16_untracked(const void* global, void* l
 // 91 us), where L2 -> LDS traffic rather than latency bounds the kernel.
 //
 // WM x WN waves of BM / WM x BN / WN wave tiles and S stages: 2 x 2 waves
-// and two stages for the 128 x 128 and 64 x 64 tiles (two blocks per CU);
-// 4 x 2 waves and three 48 KiB stages for 256 x 128 (one block per CU, a
-// quarter fewer bytes per flop, two stages in flight): C3 gate/up 125 ->
-// 119 us.  More stages at 128 x 128 (one block per CU) measured slower.
+// and two stages (two blocks per CU) for 64 x 64 and 128 x 128 tiles; 4 x 2
+// waves and three stages (one block per CU) for 256 x 128 (48 KiB stages: a
+// quarter fewer bytes per flop, two stages in flight; C3 gate/up 125 ->
+// 115 us) and for 128 x 128 where there are just enough tiles for one per
+// CU (C3 o and down: 32 -> 27 us, 83 -> 63 us).  Three or four stages of
+// 4-wave 128 x 128 tiles (one block per CU) measured slower.
 template <typename T, int BM, int BN, bool SILU, bool RES, bool UT, int WM = 2, int WN = 2, int S = kStages>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(KArgs a) {
   using E = Elem<T>;

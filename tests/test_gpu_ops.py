@@ -126,6 +126,36 @@ def test_structural_program_cache_and_leaf_aliasing(hip):
     np.testing.assert_allclose((left + right).numpy(compiler="hip"), [11.0, 22.0])
 
 
+def test_programs_sharing_a_plan_and_repeated_runs(hip):
+    """Programs of one structure share a plan (the structural program
+    cache): running one after the other rebinds each program's own leaves,
+    and a run repeated with the same device arrays (the resident-loop fast
+    path) reads what was uploaded into them since."""
+    announce("shared plans and repeated runs")
+    a = Tensor(np.array([1.0, 2.0], np.float32))
+    b = Tensor(np.array([10.0, 20.0], np.float32))
+    pa = compile_graph((a * 2.0).relu(), compiler="hip")
+    pb = compile_graph((b * 2.0).relu(), compiler="hip")
+    for _ in range(2):
+        np.testing.assert_allclose(pa()[0], [2.0, 4.0])
+        np.testing.assert_allclose(pb()[0], [20.0, 40.0])
+    source = Tensor(np.array([1.0, -3.0], np.float32))
+    program = compile_graph((source * 3.0).relu(), compiler="hip", dynamic_inputs=(source,))
+    bound = hip.device.array(np.array([1.0, 2.0], np.float32))
+    out = [hip.device.empty((2,), np.float32)]
+    first = program.run({source._node: bound}, out=out, synchronize=True)
+    np.testing.assert_allclose(hip.device.to_numpy(first[0]), [3.0, 6.0])
+    hip.device.upload(bound, np.array([-1.0, 5.0], np.float32))
+    again = program.run({source._node: bound}, out=out, synchronize=True)
+    assert again[0] is first[0]
+    np.testing.assert_allclose(hip.device.to_numpy(again[0]), [0.0, 15.0])
+    other = hip.device.array(np.array([4.0, 4.0], np.float32))
+    np.testing.assert_allclose(hip.device.to_numpy(program.run({source._node: other}, out=out, synchronize=True)[0]),
+                               [12.0, 12.0])
+    np.testing.assert_allclose(hip.device.to_numpy(program.run({source._node: bound}, out=out, synchronize=True)[0]),
+                               [0.0, 15.0])
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, BFLOAT16])
 @pytest.mark.parametrize("rows,layout", [(1, "sequence")] + [(r, l) for r in (2, 3, 5, 8) for l in ("sequence", "batch")])
 def test_gemv_linear_variants(hip, dtype, rows, layout):

@@ -404,6 +404,46 @@ def test_prefill_gemm_epilogues_match_oracle(hip, dtype, S):
         np.testing.assert_allclose(as_float(value), as_float(reference), rtol=2e-2, atol=3e-2)
 
 
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+def test_gemm_8_wave_tiles_with_epilogues(hip, dtype):
+    """The 8-wave GEMM tiles with their fused epilogues: the SiLU pair over
+    512 tiles of 256 x 128 (gate and up rows interleaved per fragment) and
+    the residual epilogue over 256 tiles of 128 x 128 (the last row of tiles
+    ragged), against float32 products of the same rounded inputs with the
+    portable graph's rounding points."""
+    from chomikgrad._planner import K_GEMM
+
+    announce(f"gemm 8-wave tiles with epilogues {dtype_name(dtype)}")
+    rng = np.random.default_rng(5)
+    K = 192
+
+    def rounded(values):
+        return as_float(as_dtype(np.asarray(values, np.float32), dtype))
+
+    x1 = as_dtype(rng.normal(size=(1, 1024, K)).astype(np.float32), dtype)
+    wg = as_dtype((rng.normal(size=(8192, K)) * 0.05).astype(np.float32), dtype)
+    wu = as_dtype((rng.normal(size=(8192, K)) * 0.05).astype(np.float32), dtype)
+    x2 = as_dtype(rng.normal(size=(1, 1960, K)).astype(np.float32), dtype)
+    wo = as_dtype((rng.normal(size=(2048, K)) * 0.05).astype(np.float32), dtype)
+    h = as_dtype(rng.normal(size=(1, 1960, 2048)).astype(np.float32), dtype)
+    X1, WG, WU, X2, WO, Hh = (Tensor(v) for v in (x1, wg, wu, x2, wo, h))
+    gate = X1 @ WG.T
+    act = gate / (1 + (-gate).exp()) * (X1 @ WU.T)
+    res = Hh + X2 @ WO.T
+    program = compile_graph(act, res, compiler="hip")
+    gemms = [st for st in program._planned.steps if st.kind == K_GEMM]
+    assert len(gemms) == 2 and sum(g.attrs.get("up") is not None for g in gemms) == 1
+    got_act, got_res = program()
+    g = rounded(as_float(x1)[0] @ as_float(wg).T)
+    u = rounded(as_float(x1)[0] @ as_float(wu).T)
+    denom = rounded(rounded(np.exp(-g)) + 1)
+    want_act = rounded(rounded(g / denom) * u)
+    want_res = rounded(as_float(h)[0] + rounded(as_float(x2)[0] @ as_float(wo).T))
+    tolerance = dict(rtol=1e-2, atol=1e-2) if dtype == np.float16 else dict(rtol=2e-2, atol=2e-2)
+    np.testing.assert_allclose(as_float(got_act).reshape(want_act.shape), want_act, **tolerance)
+    np.testing.assert_allclose(as_float(got_res).reshape(want_res.shape), want_res, **tolerance)
+
+
 def test_safetensors_bf16_stored_tensor_on_device(hip, tmp_path):
     """A BF16-stored tensor uploaded as bfloat16 (bits unchanged) and as
     float32 (exact widening), read back through the adapter."""

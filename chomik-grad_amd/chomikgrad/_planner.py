@@ -57,6 +57,9 @@ MAX_EW_INPUTS = 6
 MAX_EW_OPS = 24
 GEMV_MAX_ROWS = 8
 GEMV_STAGE_BYTES = 48 * 1024
+# batches of 2..8 independent rows on the row-exact kernels where they beat
+# the MFMA kernel (lower_linear); 0 keeps every batch GEMV on MFMA
+GEMV_BATCH_ROW_EXACT = os.environ.get("CHOMIK_HIP_GEMV_BATCH_ROW_EXACT", "1") != "0"
 # Waves sharing one GEMV row group (K split): 0 lets the kernel choose from
 # the row count; CHOMIK_HIP_GEMV_SPLIT=1/2/4 forces one (for tuning sweeps).
 GEMV_SPLIT = int(os.environ.get("CHOMIK_HIP_GEMV_SPLIT", "0"))
@@ -748,7 +751,8 @@ class Emitter:
         # a verification block) are computed row-exactly: each row with the
         # arithmetic the single-token decode step uses, so a verified token
         # is the one greedy decoding would produce.  Batches of independent
-        # sequences ((B, 1, K)) keep the MFMA kernel.
+        # sequences ((B, 1, K)) take the MFMA kernel unless
+        # choose_batch_row_exact moves them (after sibling merging).
         exact = (x.itemsize == 2 and len(x.shape) == 3 and x.shape[0] == 1
                  and 2 <= x.shape[1] <= 8 and rows == x.shape[1])
         self.add(K_GEMV, [x], [out], segments=[{"w": w, "out": out, "res": None}],
@@ -1451,6 +1455,29 @@ def merge_sibling_gemms(steps: List[Step]) -> List[Step]:
     return [s for s in steps if id(s) not in removed]
 
 
+def choose_batch_row_exact(steps: List[Step]) -> List[Step]:
+    """Batch GEMVs (2..8 independent rows, 16-bit, K <= 2048) that run on
+    the row-exact kernels, where those measured faster than the MFMA kernel
+    (C4, batch 8, K = 2048): narrow launches (o_proj 2048x2048: 6.1 against
+    7.5 us) and very tall ones (the 128256-row lm_head: 105 against
+    112 us); the merged q/k/v (3072 rows: 13.8 against 10.2 us) and the
+    gate/up pair (2 x 8192) stay on MFMA.  Decided on the merged launch, by
+    the rows of all its segments."""
+    if not GEMV_BATCH_ROW_EXACT:
+        return steps
+    for step in steps:
+        a = step.attrs
+        if step.kind != K_GEMV or a.get("exact"):
+            continue
+        x = a["prologue"]["x"] if a["prologue"] else step.ins[0]
+        if x.itemsize != 2 or not 2 <= a["rows"] <= 8 or a["K"] > 2048:
+            continue
+        n = sum(seg["w"].shape[0] for seg in a["segments"])
+        if n <= 2048 or n >= 32768:
+            a["exact"] = True
+    return steps
+
+
 def merge_sibling_gemvs(steps: List[Step]) -> List[Step]:
     removed = set()
     for i, first in enumerate(steps):
@@ -1840,6 +1867,7 @@ def plan_graph(compiler, outputs: Sequence[LazyNode], dynamic_inputs: Sequence[L
     steps = fuse_residual(steps, out_pvs)
     steps = fuse_gemm_epilogues(steps, out_pvs)
     steps = merge_sibling_gemvs(steps)
+    steps = choose_batch_row_exact(steps)
     steps = merge_sibling_gemms(steps)
     steps = fuse_decode_attention(steps, out_pvs, emitter)
     steps = fuse_block_attention(steps, out_pvs, emitter)

@@ -157,13 +157,20 @@ def test_programs_sharing_a_plan_and_repeated_runs(hip):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, BFLOAT16])
-@pytest.mark.parametrize("rows,layout", [(1, "sequence")] + [(r, l) for r in (2, 3, 5, 8) for l in ("sequence", "batch")])
-def test_gemv_linear_variants(hip, dtype, rows, layout):
+@pytest.mark.parametrize("rows,layout", [(1, "sequence")] + [(r, l) for r in (2, 3, 5, 8)
+                                                            for l in ("sequence", "batch", "batch-row-exact")])
+def test_gemv_linear_variants(hip, dtype, rows, layout, monkeypatch):
     """Few-row linears with RMSNorm prologue, residual and SiLU-pair
     epilogues against the oracle.  ``sequence``: x of shape (1, rows, K), the
     positions of one sequence (the row-exact kernel for 16-bit types);
-    ``batch``: (rows, 1, K), independent sequences (the MFMA kernel).  One
-    row is the same graph in both layouts."""
+    ``batch``: (rows, 1, K), independent sequences on the MFMA kernel;
+    ``batch-row-exact``: the same on the row-exact kernel, which the planner
+    picks for narrow batch matrices.  One row is the same graph in every
+    layout."""
+    from chomikgrad import _planner
+
+    monkeypatch.setattr(_planner, "GEMV_BATCH_ROW_EXACT", layout == "batch-row-exact")
+    monkeypatch.setattr(hip, "_program_cache", {})  # plans depend on the setting, the cache key does not
     announce(f"gemv {np.dtype(dtype)} rows={rows} {layout}")
     rng = np.random.default_rng(rows)
     K, N = 512, 384
@@ -182,6 +189,8 @@ def test_gemv_linear_variants(hip, dtype, rows, layout):
     outputs = [x @ w1.T, h + (x @ w1.T), act, act @ w3.T]
     program = compile_graph(*outputs, compiler="hip")
     assert "gemv" in program.source
+    if dtype != np.float32 and rows > 1:
+        assert ("row_exact" in program.source) == (layout != "batch")
     got = program()
     expected = realize(*outputs, compiler="cpu")
     tolerance = 1e-4 if dtype == np.float32 else 3e-2
@@ -236,6 +245,8 @@ def test_mfma_gemv_rmsnorm_prologue_equals_separate_norm(hip, dtype, rows, K, mo
     split K alike at these sizes, so the sums are added in the same order)."""
     from chomikgrad import _planner
 
+    monkeypatch.setattr(_planner, "GEMV_BATCH_ROW_EXACT", False)  # N = 208 would take the row-exact kernel
+    monkeypatch.setattr(hip, "_program_cache", {})
     announce(f"gemv mfma prologue {np.dtype(dtype)} rows={rows} K={K}")
     rng = np.random.default_rng(K + rows)
     N = 208  # 13 column tiles: a partial block of tiles where several share a block

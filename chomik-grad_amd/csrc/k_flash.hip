@@ -29,6 +29,8 @@
 #include "chip.h"
 #include "chomik_hip.h"
 
+#include <cstdlib>
+
 namespace chip {
 namespace {
 
@@ -56,13 +58,39 @@ template <> struct FlashMfma<bf16_t> {
   __device__ static __forceinline__ uint32_t bits(float v) { return f32_to_bf16_bits(v); }
 };
 
+// Block -> (batch x head, query tile).  A causal query tile qt costs qt + 1
+// key tiles, and consecutive workgroups go to the eight XCDs in turn, so
+// the plain order (tiles of one head in a row, longest first) hands XCD x
+// only tiles Q-1-x and Q-1-x-8 (at 16 tiles: 1.4x the mean work on XCD 0,
+// 0.6x on XCD 7).  The balanced order (BH a multiple of 16, Q even) gives
+// every XCD each tile BH/8 times, and pairs tile qt with Q-1-qt (the same
+// work sum) both for neighbouring blocks of an XCD and for blocks half an
+// XCD's share apart, the two ways an XCD may put two blocks on one CU.
+// Per XCD x = bid % 8, block j = bid / 8 of J = BH Q / 8: half s = (j >=
+// J/2), then j' = 2 k + e; k = rep (Q/2) + m; the tile is Q-1-m (the long
+// one) if e == s, else m; the head index is x + 8 (2 rep + s).
+__device__ __forceinline__ void block_tile(int64_t bid, int64_t BH, int64_t Q, bool balanced, int64_t& qt, int64_t& bh) {
+  if (!balanced) {
+    qt = Q - 1 - bid % Q;  // longest (causal) rows first
+    bh = bid / Q;
+    return;
+  }
+  const int64_t x = bid & 7, j = bid >> 3, half = BH * Q / 16;
+  const int64_t s = j >= half ? 1 : 0, jp = j - s * half;
+  const int64_t e = jp & 1, k = jp >> 1, P = Q / 2;
+  const int64_t m = k % P, rep = k / P;
+  qt = e == s ? Q - 1 - m : m;
+  bh = x + 8 * (2 * rep + s);
+}
+
 // K_SDPA layout (shared with k_sdpa): p[0] q, p[1] K, p[2] V, p[3] mask (or
 // null), p[4] out (B, H, T, 64).  n[0] B, n[1] H, n[2] T, n[3] C, n[4] hd,
 // n[5] KV, n[6] dtype, n[7..10] q strides (b, h, t, d), n[11..14] K strides
 // (b, kv, c, d), n[15..18] V strides, n[19..22] mask strides (b, h, t, c),
 // n[23] mask dtype, n[24] causal mask proved, n[25] q, K, V views start on
-// 16-byte boundaries, n[26..28] out strides (b, h, t; unit along hd);
-// f[0] d, f[1] the causal mask's value above the diagonal.
+// 16-byte boundaries, n[26..28] out strides (b, h, t; unit along hd),
+// n[29] block order (set by plan_flash_prefill); f[0] d, f[1] the causal
+// mask's value above the diagonal.
 // At most 128 VGPRs (four waves per SIMD): two 8-wave blocks per CU.
 template <typename T>
 __global__ __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
@@ -75,10 +103,9 @@ void k_flash_prefill(KArgs a) {
   const int64_t H = a.n[1], Tq = a.n[2], C = a.n[3], KVh = a.n[5];
   const int64_t G = H / KVh;
   const int64_t qtiles = (Tq + kBQ - 1) / kBQ;
-  int64_t bid = blockIdx.x;
-  const int64_t qt = qtiles - 1 - bid % qtiles;  // longest (causal) rows first
-  bid /= qtiles;
-  const int64_t h = bid % H, b = bid / H, g = h / G;
+  int64_t qt, bh;
+  block_tile(static_cast<int64_t>(blockIdx.x), a.n[0] * H, qtiles, a.n[29] != 0, qt, bh);
+  const int64_t h = bh % H, b = bh / H, g = h / G;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, fi = lane & 15, fg = lane >> 4;
   const int64_t q0 = qt * kBQ;
   const int64_t my_q = q0 + 16 * w + fi;  // the query of this lane's score column
@@ -269,8 +296,16 @@ bool plan_flash_prefill(KArgs& a, Launch& l) {
   // (planners run before pointers are bound: decide from the integers; the
   // step always carries a mask, read unless the causal triangle was proved)
   if (a.n[24] == 0 && a.n[23] != dt) return false;
-  const int64_t blocks = a.n[0] * a.n[1] * ((a.n[2] + kBQ - 1) / kBQ);
+  const int64_t qtiles = (a.n[2] + kBQ - 1) / kBQ;
+  const int64_t blocks = a.n[0] * a.n[1] * qtiles;
   if (blocks <= 0 || blocks > 2147483647) return false;
+  // balanced block order where the causal work differs per tile and the
+  // shape allows it (CHOMIK_HIP_FLASH_BALANCED=0 keeps the plain order)
+  static const bool balanced_knob = [] {
+    const char* v = getenv("CHOMIK_HIP_FLASH_BALANCED");
+    return !(v && *v && atoi(v) == 0);
+  }();
+  a.n[29] = balanced_knob && a.n[24] != 0 && (a.n[0] * a.n[1]) % 16 == 0 && qtiles % 2 == 0 ? 1 : 0;
   l.func = dt == F16 ? reinterpret_cast<const void*>(&k_flash_prefill<__half>)
                      : reinterpret_cast<const void*>(&k_flash_prefill<bf16_t>);
   l.grid = dim3(static_cast<unsigned>(blocks));

@@ -318,16 +318,19 @@ def _sdpa_graph(q, k, v, mask, heads, dtype):
 
 
 @pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
-@pytest.mark.parametrize("T,mask_kind", [(100, "causal"), (300, "causal"), (70, "dense")])
-def test_prefill_attention_matches_oracle(hip, dtype, T, mask_kind):
+@pytest.mark.parametrize("T,mask_kind,H", [(100, "causal", 8), (300, "causal", 8), (70, "dense", 8),
+                                           (400, "causal", 16)])
+def test_prefill_attention_matches_oracle(hip, dtype, T, mask_kind, H):
     """Prefill attention (K_SDPA with 16+ query rows, head size 64) runs the
     MFMA kernel: a captured causal triangle is proved and applied
     arithmetically (tiles above the diagonal skipped); any other mask is read
-    from memory.  Ragged T covers partial query and key tiles; 8 query heads
-    over 2 KV heads covers GQA."""
-    announce(f"prefill attention {dtype_name(dtype)} T={T} {mask_kind}")
+    from memory.  Ragged T covers partial query and key tiles; 8 (16) query
+    heads over 2 (4) KV heads covers GQA.  16 heads over an even number of
+    128-row query tiles take the balanced block order (tile qt beside tile
+    Q-1-qt), the others the plain order."""
+    announce(f"prefill attention {dtype_name(dtype)} T={T} {mask_kind} H={H}")
     rng = np.random.default_rng(T)
-    H, KV = 8, 2
+    KV = H // 4
     q = Tensor(as_dtype(rng.normal(size=(1, H, T, 64)).astype(np.float32), dtype), copy=False)
     k = Tensor(as_dtype(rng.normal(size=(1, KV, T, 64)).astype(np.float32), dtype), copy=False)
     v = Tensor(as_dtype(rng.normal(size=(1, KV, T, 64)).astype(np.float32), dtype), copy=False)

@@ -3,7 +3,10 @@
 // one sweep over the key tiles with an online softmax (running maximum and
 // sum, rescaled as the maximum grows; FlashAttention-2's recurrence) in
 // float32, rounded once to the output dtype.  Scores are scaled into the
-// base-2 domain (s * log2(e) / d) so every exponential is one exp2.
+// base-2 domain (s * log2(e) / d) so every exponential is one v_exp_f32
+// (__builtin_amdgcn_exp2f: exp2f adds a compare, two selects and an ldexp
+// per call to keep results below 2^-126, terms 1e-38 of the running maximum
+// that no sum or fp16/bf16 output can show).
 //
 // Block = 512 threads = 8 wavefronts, 128 query rows (16 per wave), key
 // tiles of 64: one K/V tile in LDS serves eight waves' MFMA work.  Scores are computed transposed, S^T = K Q^T with
@@ -203,7 +206,7 @@ void k_flash_prefill(KArgs a) {
     const float mnew = fmaxf(m, tmax);
     // every query has an unmasked key in its first tile, so mnew is finite
     // from the first tile on (a -inf - -inf would need an all-masked row)
-    const float alpha = exp2f((m - mnew) * scale);
+    const float alpha = __builtin_amdgcn_exp2f((m - mnew) * scale);
     m = mnew;
     const float mscaled = mnew * scale;
     float p[4][4];
@@ -212,7 +215,7 @@ void k_flash_prefill(KArgs a) {
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[t][r] = exp2f(fmaf(x[t][r], scale, -mscaled));
+        p[t][r] = __builtin_amdgcn_exp2f(fmaf(x[t][r], scale, -mscaled));
         psum += p[t][r];
       }
     lsum = lsum * alpha + psum;

@@ -347,6 +347,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(KArgs a) {
   // at the top of iteration k every wave has finished stage k - 1, whose
   // buffer that issue reuses
   const int nst = static_cast<int>(K / kBK);
+  const bool late = UT && a.n[24] != 0;
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < nst) load_stage(int64_t(st) * kBK, st);
@@ -358,7 +359,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(KArgs a) {
     else if (later == 1) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AI + WI) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (k + S - 1 < nst) load_stage(int64_t(k + S - 1) * kBK, (k + S - 1) % S);
+    // late (n[24], untracked loads only): the stage loads are issued after
+    // the first k-substep's MFMAs, so the fragment reads after the barrier
+    // come first; tracked loads there would make the second substep's reads
+    // wait for them
+    if (!late && k + S - 1 < nst) load_stage(int64_t(k + S - 1) * kBK, (k + S - 1) % S);
     const int buf = k % S;
 #pragma unroll
     for (int ks = 0; ks < kBK / 32; ++ks) {
@@ -378,6 +383,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(KArgs a) {
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::step(fa[i], fw[j], acc[i][j]);
+      if (late && ks == 0 && k + S - 1 < nst) load_stage(int64_t(k + S - 1) * kBK, (k + S - 1) % S);
     }
   }
 
@@ -496,6 +502,14 @@ const char* plan_gemm(KArgs& a, Launch& l) {
   const int64_t tiles = ((M + bm - 1) / bm) * ((N + on - 1) / on);
   const int64_t blocks = 8 * ((tiles + 7) / 8);
   if (blocks > 2147483647) return "gemm: too many tiles";
+  // stage loads issued late in the stage (CHOMIK_HIP_GEMM_LATE: 0 never,
+  // 1 the three-stage 8-wave tiles, 2 every untracked tile)
+  static const int late_knob = [] {
+    const char* v = std::getenv("CHOMIK_HIP_GEMM_LATE");
+    return v && *v ? std::atoi(v) : 1;
+  }();
+  const bool eight = lds && (tile == kTile256x8 || tile == kTile128x8);
+  a.n[24] = late_knob >= 2 || (late_knob == 1 && eight) ? 1 : 0;
   l.func = dt == F16 ? pick_gemm<__half>(tile, silu, res, lds, long_k) : pick_gemm<bf16_t>(tile, silu, res, lds, long_k);
   l.grid = dim3(static_cast<unsigned>(blocks));
   l.block = dim3(lds && (tile == kTile256x8 || tile == kTile128x8) ? 512 : 256);

@@ -427,15 +427,28 @@ def main() -> int:
     prompt = synthetic.prompt_ids(config.vocab_size, PROMPT, seed=0)
     context = PROMPT + 1 + args.warmup + args.steps + args.timing_runs
 
-    # Prefill (compile + one warm run, then one timed run).
+    lib = hip.lib
+    # Prefill (compile + one warm run, then one timed run: HIP events on the
+    # library stream, and the host's wall clock, which also holds the cache
+    # allocation and the uploads).
     runtime.prefill(prompt, context)
     device.synchronize()
     log("prefill compiled")
+    start_event, stop_event = ctypes.c_void_p(), ctypes.c_void_p()
+    lib.call("chip_event_create", ctypes.byref(start_event))
+    lib.call("chip_event_create", ctypes.byref(stop_event))
     t0 = time.perf_counter()
+    lib.call("chip_event_record", start_event)
     logits, caches = runtime.prefill(prompt, context)
+    lib.call("chip_event_record", stop_event)
     device.synchronize()
-    prefill_seconds = time.perf_counter() - t0
-    log(f"prefill {PROMPT} tokens: {prefill_seconds * 1e3:.1f} ms")
+    prefill_wall_ms = (time.perf_counter() - t0) * 1e3
+    prefill_event_ms = ctypes.c_float(0.0)
+    lib.call("chip_event_elapsed_ms", start_event, stop_event, ctypes.byref(prefill_event_ms))
+    lib.call("chip_event_destroy", start_event)
+    lib.call("chip_event_destroy", stop_event)
+    prefill_ms = prefill_event_ms.value
+    log(f"prefill {PROMPT} tokens: {prefill_ms:.2f} ms on the stream ({prefill_wall_ms:.1f} ms host wall)")
 
     history = device.empty((1 + args.warmup + args.steps + args.timing_runs,), np.int32)
     token = device.empty((1, 1), np.int32)
@@ -464,7 +477,6 @@ def main() -> int:
 
     decode(args.warmup)
     device.synchronize()
-    lib = hip.lib
     start_event, stop_event = ctypes.c_void_p(), ctypes.c_void_p()
     lib.call("chip_event_create", ctypes.byref(start_event))
     lib.call("chip_event_create", ctypes.byref(stop_event))
@@ -572,7 +584,8 @@ def main() -> int:
         "step_roofline": {"bytes_per_token": int(bytes_per_token), "achieved_gbps": round(step_gbps, 1),
                           "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
         "gpu_event_ms_per_step": round(gpu_ms.value / args.steps, 4),
-        "prefill_tok_per_s": round(PROMPT / prefill_seconds, 1),
+        "prefill_tok_per_s": round(PROMPT / (prefill_ms * 1e-3), 1),
+        "prefill_ms": {"stream_events": round(prefill_ms, 3), "host_wall": round(prefill_wall_ms, 2)},
         "prefill_c3": prefill_c3,
         "c4_batched_decode": c4,
         "c5_speculative": c5,

@@ -47,6 +47,12 @@ constexpr int kKRow = kD + 8;   // LDS row of the K tile (elements)
 // P V operand read touches fall on distinct banks (C3 launch: 6.7e6 -> 2.2e6
 // bank-conflict cycles against 36 words)
 constexpr int kVRow = kBK + 4;
+// Dimension d of V lives in LDS row vt_row(d): bits 2 and 3 swapped.  A store
+// instruction has even lanes writing dimension d and odd lanes d + 4; their
+// rows are then 8 apart (272 words, the other half of the banks) instead of
+// 4 (136 words, an 8-bank overlap).  Any 16 consecutive dimensions still
+// occupy 16 consecutive rows, so the operand reads keep distinct banks.
+__device__ __forceinline__ int vt_row(int d) { return (d & ~12) | ((d & 4) << 1) | ((d & 8) >> 1); }
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T> struct FlashMfma;
@@ -160,7 +166,7 @@ void k_flash_prefill(KArgs a) {
     const uint32_t r1 = static_cast<uint32_t>(dpp_move(static_cast<int>(odd ? t.v.y : t.v.w), 0xB1));
     const uint32_t lo0 = odd ? r0 : t.v.x, lo1 = odd ? r1 : t.v.y;  // key 2j
     const uint32_t hi0 = odd ? t.v.z : r0, hi1 = odd ? t.v.w : r1;  // key 2j + 1
-    uint32_t* vw = reinterpret_cast<uint32_t*>(Vt) + (8 * vc + (odd ? 4 : 0)) * (kVRow / 2) + (vr >> 1);
+    uint32_t* vw = reinterpret_cast<uint32_t*>(Vt) + vt_row(8 * vc + (odd ? 4 : 0)) * (kVRow / 2) + (vr >> 1);
     vw[0] = (lo0 & 0xffffu) | (hi0 << 16);
     vw[kVRow / 2] = (lo0 >> 16) | (hi0 & 0xffff0000u);
     vw[kVRow] = (lo1 & 0xffffu) | (hi1 << 16);
@@ -252,7 +258,7 @@ void k_flash_prefill(KArgs a) {
       const uint4 pa = make_uint4(pw[0], pw[1], pw[2], pw[3]);
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
-        const uint16_t* row = &Vt[(16 * tn + fi) * kVRow];
+        const uint16_t* row = &Vt[(16 * tn + vt_row(fi)) * kVRow];
         const uint2 lo = *reinterpret_cast<const uint2*>(row + 32 * c + 4 * fg);
         const uint2 hi = *reinterpret_cast<const uint2*>(row + 32 * c + 16 + 4 * fg);
         o[tn] = F::step(pa, make_uint4(lo.x, lo.y, hi.x, hi.y), o[tn]);

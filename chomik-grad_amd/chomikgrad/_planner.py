@@ -60,6 +60,7 @@ GEMV_STAGE_BYTES = 48 * 1024
 # batches of 2..8 independent rows on the row-exact kernels where they beat
 # the MFMA kernel (lower_linear); 0 keeps every batch GEMV on MFMA
 GEMV_BATCH_ROW_EXACT = os.environ.get("CHOMIK_HIP_GEMV_BATCH_ROW_EXACT", "1") != "0"
+GEMV_BATCH_ROW_EXACT_MAX_K = int(os.environ.get("CHOMIK_HIP_GEMV_BATCH_ROW_EXACT_MAX_K", "2048"))
 # Waves sharing one GEMV row group (K split): 0 lets the kernel choose from
 # the row count; CHOMIK_HIP_GEMV_SPLIT=1/2/4 forces one (for tuning sweeps).
 GEMV_SPLIT = int(os.environ.get("CHOMIK_HIP_GEMV_SPLIT", "0"))
@@ -1470,7 +1471,7 @@ def choose_batch_row_exact(steps: List[Step]) -> List[Step]:
         if step.kind != K_GEMV or a.get("exact"):
             continue
         x = a["prologue"]["x"] if a["prologue"] else step.ins[0]
-        if x.itemsize != 2 or not 2 <= a["rows"] <= 8 or a["K"] > 2048:
+        if x.itemsize != 2 or not 2 <= a["rows"] <= 8 or a["K"] > GEMV_BATCH_ROW_EXACT_MAX_K:
             continue
         n = sum(seg["w"].shape[0] for seg in a["segments"])
         if n <= 2048 or n >= 32768:

@@ -18,10 +18,11 @@
 // O[query 4 g + r][dim 16 n + i] in lane (i, g); a query's rescale factor
 // comes from the lane that owns its scores (one shuffle per row).  V goes
 // through LDS transposed ([dim][key]) to supply the B operand, written as
-// 32-bit words of two consecutive keys.  K and V tiles are loaded two ahead into two register sets used
-// in turn (the loop handles two tiles per iteration, so every wait covers
-// exactly the set about to be stored); loads past the last tile re-read it
-// and keys past the cache are clamped and zeroed, so no load is conditional.
+// 32-bit words of two consecutive keys.  K and V tiles are loaded two ahead
+// into two register sets used in turn (the loop handles two tiles per
+// iteration, so every wait covers exactly the set about to be stored); loads
+// past the last tile re-read it and keys past the cache are clamped and
+// zeroed, so no load is conditional.
 //
 // When the planner has proved the mask is the causal triangle (0 on and below
 // the diagonal, one value v <= -1e4 above), key tiles above the diagonal are

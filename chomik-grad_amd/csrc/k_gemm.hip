@@ -59,8 +59,9 @@ template <> struct Mfma<bf16_t> {
 // epilogue (elements; the planner picks the kernel from these flags, the
 // pointers are bound later), n[11] output segments (0 or 1: one), n[12..15]
 // their widths (multiples of 128: a tile lies in one segment), n[16..19]
-// their ldc, n[20..23] their ldw.  Segments are sibling products of the
-// same A (q, k and v projections) in one launch; plain epilogue only.
+// their ldc, n[20..23] their ldw; n[24] (set by plan_gemm) issues the
+// stage loads after the first k-substep.  Segments are sibling products of
+// the same A (q, k and v projections) in one launch; plain epilogue only.
 // Epilogues (the portable graph's rounding points, as in the decode GEMVs):
 //  * RES:  C = round(R + round(acc))
 //  * SILU: the tile's weight rows alternate, 16 at a time, between the gate

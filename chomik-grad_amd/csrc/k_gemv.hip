@@ -585,10 +585,20 @@ __global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) ss = W::dot(W::mul(xw[u][i], xw[u][i]), W::kOnes, ss);
         const float total = E::round(wave_sum(ss));
-        const float mean = E::round(total / E::round(static_cast<float>(K)));
+        // a power-of-two K divides exactly by scaling (the quotient of a
+        // 16-bit total is exact in fp32); the branch is uniform
+        float mean;
+        if ((K & (K - 1)) == 0) mean = E::round(ldexpf(total, -static_cast<int>(__builtin_ctzll(K))));
+        else mean = E::round(total / E::round(static_cast<float>(K)));
         const float rn = E::round(sqrtf(E::round(mean + E::round(a.f[0]))));
-        const float inv = 1.0f / rn;
         if constexpr (W::kNoBranch) {
+          // The quotient routine takes 1 / rn to within 2 ulp, so the
+          // hardware reciprocal (1 ulp) serves it and the IEEE division
+          // stays off the prologue's dependency chain.  An fp16 rn is never
+          // subnormal (the square root of the least fp16 is 2^-12): it is a
+          // fast divisor, or 0, infinite or NaN, whose reciprocals v_rcp_f32
+          // returns exactly, so x * inv stays their IEEE quotient.
+          const float inv = __builtin_amdgcn_rcpf(rn);
           const bool corrected = W::fast_divisor(rn);
 #pragma unroll
           for (int u = 0; u < VPL; ++u) {
@@ -602,6 +612,7 @@ __global__ __launch_bounds__(256) void k_gemv_row(KArgs a) {
             }
           }
         } else {
+          const float inv = 1.0f / rn;
           bool fast = W::fast_divisor(rn);
 #pragma unroll
           for (int u = 0; u < VPL; ++u)

@@ -233,6 +233,48 @@ def test_gemv_split_over_blocks(hip, dtype, rows, K, N):
 
 
 @pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("K", [320, 768, 2048])
+def test_row_gemv_rmsnorm_prologue_equals_separate_norm(hip, dtype, K, monkeypatch):
+    """One decode row: the RMSNorm folded into the row GEMV's prologue gives
+    the bits of the separate rms_norm step followed by the same GEMV.  The
+    prologue takes the mean of a power-of-two K by scaling (K = 2048, the
+    C2 width) and divides otherwise (K = 320 and 768, whose rows also end
+    inside a 16-byte vector group), and its quotient routine runs on the
+    hardware reciprocal of rn.  Inputs are multiples of 1/8 in [-2, 2], so
+    every float32 sum of squares is exact in any order and both paths round
+    the same total; the norm weight is not constant."""
+    from chomikgrad import _planner
+
+    monkeypatch.setattr(hip, "_program_cache", {})
+    announce(f"gemv row prologue {np.dtype(dtype)} K={K}")
+    rng = np.random.default_rng(K)
+    N = 200
+    x = Tensor((rng.integers(-16, 17, size=(1, 1, K)) / 8).astype(np.float32), dtype=dtype)
+    h = Tensor(rng.normal(size=(1, 1, N)).astype(np.float32), dtype=dtype)
+    norm = Tensor(rng.normal(1.0, 0.3, size=K).astype(np.float32), dtype=dtype)
+    w1, w2, w3 = (Tensor((rng.normal(size=(N, K)) * 0.05).astype(np.float32), dtype=dtype) for _ in range(3))
+    variance = (x * x).mean(axis=-1, keepdims=True)
+    normed = x / (variance + 1e-5).sqrt() * norm
+    normed._node.lowering = ("rms_norm", (x._node, norm._node), 1e-5)
+    gate = normed @ w1.T
+    outputs = [h + normed @ w3.T, gate / (1 + (-gate).exp()) * (normed @ w2.T)]
+    fused = compile_graph(*outputs, compiler="hip")
+    assert " rms_norm(" not in fused.source and fused.source.count("gemv[rms_norm") == 2
+    assert "row_exact" not in fused.source
+    got = fused()
+    monkeypatch.setattr(_planner, "fuse_rmsnorm_prologue", lambda steps, outputs: steps)
+    monkeypatch.setattr(hip, "_program_cache", {})  # plan again rather than reuse the fused program
+    separate = compile_graph(*outputs, compiler="hip")
+    assert " rms_norm(" in separate.source
+    want = separate()
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(np.asarray(g).view(np.uint16), np.asarray(w).view(np.uint16))
+    expected = realize(*outputs, compiler="cpu")
+    for g, e in zip(got, expected):
+        np.testing.assert_allclose(as_float(g), as_float(e), rtol=3e-2, atol=3e-2)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, BFLOAT16], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("rows,K", [(2, 96), (3, 128), (5, 256), (8, 512), (8, 1024)])
 def test_mfma_gemv_rmsnorm_prologue_equals_separate_norm(hip, dtype, rows, K, monkeypatch):
     """A batch's RMSNorm folded into the MFMA GEMV as its prologue gives the

@@ -281,6 +281,50 @@ def test_batched_bf16_decode():
         np.testing.assert_allclose(as_float(value), as_float(reference), atol=2e-2, rtol=2e-2)
 
 
+def test_batch_row_exact_choice_by_merged_launch(monkeypatch):
+    """Batch GEMVs (8 independent bf16 rows) go to the row-exact kernels
+    when the merged launch is narrow (<= 2048 output rows) or very tall
+    (>= 32768) and K <= 2048; the merged q/k/v (3072 rows), a 4096-row
+    launch and a K = 4096 projection stay on the MFMA kernel.  Planning only
+    (no kernels run); with the pass switched off nothing is row-exact."""
+    from chomikgrad import _planner
+
+    rng = np.random.default_rng(11)
+
+    def act(*shape):
+        return Tensor(to_bf16(rng.normal(size=shape)), copy=False)
+
+    def weight(n, k):
+        return Tensor(to_bf16(rng.normal(size=(n, k)) * 0.05), copy=False)
+
+    def rms(x):
+        norm = Tensor(to_bf16(rng.normal(1.0, 0.2, size=x.shape[-1])), copy=False)
+        normed = x / ((x * x).mean(axis=-1, keepdims=True) + 1e-5).sqrt() * norm
+        normed._node.lowering = ("rms_norm", (x._node, norm._node), 1e-5)
+        return normed
+
+    x, x2, a, h, b, d = act(8, 1, 64), act(8, 1, 64), act(8, 1, 64), act(8, 1, 2048), act(8, 1, 64), act(8, 1, 4096)
+    normed, normed2 = rms(x), rms(x2)
+    outputs = [normed @ weight(2048, 64).T, normed @ weight(512, 64).T, normed @ weight(512, 64).T,  # q/k/v
+               h + a @ weight(2048, 64).T,       # o_proj-like: 2048 rows with the residual
+               normed2 @ weight(32768, 64).T,    # lm_head-like: 32768 rows
+               b @ weight(4096, 64).T,           # 4096 rows
+               d @ weight(2048, 4096).T]         # K = 4096
+    dynamic = [t._node for t in (x, x2, a, h, b, d)]
+
+    def exact_rows(enabled):
+        monkeypatch.setattr(_planner, "GEMV_BATCH_ROW_EXACT", enabled)
+        planned = plan_graph(COMPILER, [t._node for t in outputs], dynamic, [])
+        gemvs = [st for st in planned.steps if st.kind == K_GEMV]
+        assert len(gemvs) == 5  # q/k/v merged into one launch
+        return {(sum(seg["w"].shape[0] for seg in st.attrs["segments"]), st.attrs["K"]): bool(st.attrs.get("exact"))
+                for st in gemvs}
+
+    assert exact_rows(True) == {(3072, 64): False, (2048, 64): True, (32768, 64): True,
+                                (4096, 64): False, (2048, 4096): False}
+    assert not any(exact_rows(False).values())
+
+
 def test_dynamic_inputs_are_validated():
     from chomikgrad.hip_backend import HIPCompiler
 

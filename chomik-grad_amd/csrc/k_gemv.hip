@@ -1992,12 +1992,13 @@ const char* plan_gemv(KArgs& a, Launch& l) {
     // 31.2 us at 4096).  Below 4096 groups, 1024 waves for rows with the
     // RMSNorm prologue or of at least 8 vectors per lane (q/k/v 8.5 -> 7.9 us,
     // down 10.5 -> 9.7 us), one group per wave otherwise (o: 5.8 against
-    // 6.0 us streamed).  CHOMIK_HIP_GEMV_EXACT_WAVES fixes the wave count
-    // (0: never stream).
+    // 6.0 us streamed); eight-row batches stream one group per wave (C4's
+    // 2048-row o projection: 5912-5918 -> 5979-5986 tok/s end to end).
+    // CHOMIK_HIP_GEMV_EXACT_WAVES fixes the wave count (0: never stream).
     static const int exact_waves = env_int("CHOMIK_HIP_GEMV_EXACT_WAVES", -1);
     const size_t run_bytes = static_cast<size_t>((M + (pro ? 1 : 0)) * K) * dtype_size(dt);
     const void* run = dt == F16 ? pick_exact_run<__half>(kv, pro, silu) : pick_exact_run<bf16_t>(kv, pro, silu);
-    const int64_t small_want = (pro || kv >= 8 * 64) ? 1024 : 0;
+    const int64_t small_want = (pro || kv >= 8 * 64) ? 1024 : M >= 8 ? groups : 0;
     const int64_t want = exact_waves >= 0 ? exact_waves : groups < 4096 ? small_want : groups < 16384 ? 2048 : 4096;
     if (run && run_bytes <= kExactStageBytes && want >= 1) {
       const int64_t nwaves = groups < want ? groups : want;
